@@ -1,0 +1,141 @@
+// collect<Env>: the whole rollout of model/ppo.h:716-751 (minus GAE) in one
+// launch. Each 256-thread workgroup owns M envs for all T steps:
+//
+//   for t in 0..T:  policy forward on the staged obs (MFMA, see policy.h)
+//                   t <  T: env lanes sample from the head with their own RNG,
+//                           reset-if-done, Env::step, write the [T][n] slots
+//                   t == T: write the bootstrap head (model/ppo.h:735)
+//
+// Env lanes are threads 0..M-1 (one wave). A small State lives in registers of
+// its lane for the whole rollout; a large one is updated in place. Per env and
+// step the RNG order is: sample draw(s), reset draws if done, then step
+// (model/ppo.h:728-730, rollout.h:46-47).
+#pragma once
+#include "policy.h"
+#include "sample.h"
+
+namespace mg {
+namespace dev {
+
+template <int M, int O, int HD>
+struct CollectSmem {
+    FwdSmem<M> fwd;
+    float obs[M * O];
+    float head[M * HD];
+};
+
+template <typename Env, int M>
+__global__ void __launch_bounds__(256, 2) collect_kernel(const mg_collect_args a) {
+    using Tr = EnvTraits<Env>;
+    using State = typename Env::State;
+    using Action = typename Env::Action;
+    using Obs = typename Env::Obs;
+    constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
+    __shared__ CollectSmem<M, O, HD> sm;
+    FwdRegs<M> R;
+
+    const int tid = threadIdx.x;
+    const uint32_t n = a.n, T = a.horizon;
+    const uint32_t i = blockIdx.x * M + (uint32_t)tid;
+    const bool envLane = tid < M;
+    State* states = static_cast<State*>(a.state);
+    Action* actSlots = static_cast<Action*>(a.action_slots);
+    const float* logStd = a.policy.params + a.policy.off_log_std;
+
+    uint32_t rng = 0;
+    uint8_t done = 0;
+    // A small State lives in this register copy; a large one is used in place.
+    std::conditional_t<Tr::STATE_IN_REGISTERS, State, char> sreg;
+    auto S = [&]() -> State& {
+        if constexpr (Tr::STATE_IN_REGISTERS)
+            return sreg;
+        else
+            return states[i];
+    };
+    float obs[O];
+
+    if (envLane) {
+        rng = a.rng[i];
+        done = a.done[i];
+        if constexpr (Tr::STATE_IN_REGISTERS) sreg = states[i];
+        if (a.first) {  // model/ppo.h:720-722: one step with action 0 into slot 0
+            Action act{};
+            if (done) Env::reset(S(), rng);
+            Obs o{};
+            float r = 0.0f;
+            Env::step(S(), act, o, r, done);
+            const float* of = reinterpret_cast<const float*>(&o);
+#pragma unroll
+            for (int k = 0; k < O; ++k) obs[k] = of[k];
+            store_floats<O>(a.obs_slots + (size_t)i * O, obs);
+            a.reward_slots[i] = r;
+        } else {  // model/ppo.h:724: obs[T] -> obs[0]
+            load_floats<O>(obs, a.obs_slots + ((size_t)T * n + i) * O);
+            store_floats<O>(a.obs_slots + (size_t)i * O, obs);
+        }
+#pragma unroll
+        for (int k = 0; k < O; ++k) sm.obs[tid * O + k] = obs[k];
+    }
+    __syncthreads();
+
+    for (uint32_t t = 0; t <= T; ++t) {
+        policy_forward<M>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
+        if (envLane) {
+            const float* h = sm.head + tid * HD;
+            if (t == T) {  // bootstrap head for GAE and headValue()
+#pragma unroll
+                for (int j = 0; j < HD; ++j) a.head_out[(size_t)i * HD + j] = h[j];
+            } else {
+                const size_t k = (size_t)t * n + i;
+                Action act;
+                float lp;
+                if constexpr (Tr::CONTINUOUS)
+                    sample_gaussian(h, logStd, A, rng, reinterpret_cast<float*>(&act), lp);
+                else
+                    act = (Action)sample_categorical(h, A, rng, lp);
+                actSlots[k] = act;
+                a.logp_slots[k] = lp;
+                a.value_slots[k] = h[A];
+                if (done) Env::reset(S(), rng);
+                Obs o{};
+                float r = 0.0f;
+                Env::step(S(), act, o, r, done);
+                const float* of = reinterpret_cast<const float*>(&o);
+#pragma unroll
+                for (int q = 0; q < O; ++q) obs[q] = of[q];
+                store_floats<O>(a.obs_slots + (k + n) * O, obs);
+                a.reward_slots[k] = r;
+                a.done_slots[k] = done;
+#pragma unroll
+                for (int q = 0; q < O; ++q) sm.obs[tid * O + q] = obs[q];
+            }
+        }
+        __syncthreads();
+    }
+    if (envLane) {
+        if constexpr (Tr::STATE_IN_REGISTERS) states[i] = sreg;
+        a.rng[i] = rng;
+        a.done[i] = done;
+    }
+}
+
+template <typename Env>
+int launch_collect(const mg_collect_args* a) {
+    if (!a || a->n == 0 || a->n % 64 != 0 || a->horizon == 0) return MG_ERR_INVALID;
+    if (a->policy.obs_dim != Env::OBS_DIM || a->policy.act_dim != Env::ACT_DIM ||
+        a->policy.embed != (uint32_t)kEmbed || a->policy.hidden % kChunk != 0 || a->policy.layers == 0 ||
+        a->policy.layers > MG_MAX_LAYERS)
+        return MG_ERR_INVALID;
+    hipStream_t st = static_cast<hipStream_t>(a->stream);
+    // 64-row tiles need n / 64 >= 2 workgroups per CU to fill the chip; smaller
+    // runs use 32-row tiles for twice the workgroups.
+    if (a->n >= 64u * 512u) {
+        hipLaunchKernelGGL((collect_kernel<Env, 64>), dim3(a->n / 64), dim3(256), 0, st, *a);
+    } else {
+        hipLaunchKernelGGL((collect_kernel<Env, 32>), dim3(a->n / 32), dim3(256), 0, st, *a);
+    }
+    return (int)hipGetLastError();
+}
+
+}  // namespace dev
+}  // namespace mg

@@ -1,0 +1,97 @@
+// Device-side building blocks shared by the env kernels (compiled per env by
+// MG_DEFINE_ENV) and by the library's policy/PPO kernels. gfx950 (CDNA4) only:
+// 64-lane wavefronts, fp32 MFMA, 160 KB LDS per CU.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../capi.h"
+#include "../env.h"
+
+namespace mg {
+namespace dev {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+constexpr int kEmbed = MG_EMBED;  // 128, compile-time as in the reference (model/config.h:7)
+
+// v_mfma_f32_32x32x2_f32: D[32x32] += A[32x2] B[2x32].
+// Operands: lane l supplies A[l % 32][l / 32] and B[l / 32][l % 32].
+// Result: register r of lane l holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+__device__ __forceinline__ f32x16 mfma32x32x2(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+// v_mfma_f32_16x16x4_f32: D[16x16] += A[16x4] B[4x16].
+// Operands: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16].
+// Result: register r of lane l holds D[4 (l / 16) + r][l % 16].
+__device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int c32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+__device__ __forceinline__ int c16_row(int r, int lane) { return 4 * (lane >> 4) + r; }
+
+// Sum over groups of G consecutive lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Store OBS_DIM floats with the widest stores the row alignment allows.
+template <int N>
+__device__ __forceinline__ void store_floats(float* dst, const float* src) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i)
+            reinterpret_cast<float4*>(dst)[i] = make_float4(src[4 * i], src[4 * i + 1], src[4 * i + 2], src[4 * i + 3]);
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) reinterpret_cast<float2*>(dst)[i] = make_float2(src[2 * i], src[2 * i + 1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) dst[i] = src[i];
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void load_floats(float* dst, const float* src) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            float4 v = reinterpret_cast<const float4*>(src)[i];
+            dst[4 * i] = v.x, dst[4 * i + 1] = v.y, dst[4 * i + 2] = v.z, dst[4 * i + 3] = v.w;
+        }
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) {
+            float2 v = reinterpret_cast<const float2*>(src)[i];
+            dst[2 * i] = v.x, dst[2 * i + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) dst[i] = src[i];
+    }
+}
+
+// A uniformly random action from the env's stream (D4 of the build plan):
+// rngInt(rng, ACT_DIM) for an integer action, uniform [-1, 1) per float.
+template <typename Env>
+__device__ __forceinline__ typename Env::Action random_action(uint32_t& rng) {
+    using Action = typename Env::Action;
+    if constexpr (EnvTraits<Env>::CONTINUOUS) {
+        Action a;
+        float* f = reinterpret_cast<float*>(&a);
+#pragma unroll
+        for (uint32_t k = 0; k < Env::ACT_DIM; ++k) f[k] = rngUniform(rng, -1.0f, 1.0f);
+        return a;
+    } else {
+        return (Action)rngInt(rng, Env::ACT_DIM);
+    }
+}
+
+}  // namespace dev
+}  // namespace mg

@@ -1,0 +1,122 @@
+// VoxelNav16: a gather-heavy 3-D navigation env.
+//
+// There is no reference code for this env; it is written from its
+// specification. The reference's examples/VoxelNav is a different heightmap
+// env. Specification:
+//   - each env owns a 16 x 16 x 16 uint8 occupancy grid (1 = occupied), each
+//     cell occupied with probability 1/4, drawn from the env's RNG at every reset;
+//   - the agent and the goal start on distinct random free cells;
+//   - 6 actions: +x, -x, +y, -y, +z, -z; a move into an occupied cell or out of
+//     the grid is blocked and the agent stays;
+//   - obs = the 3x3x3 occupancy neighbourhood around the agent as 27 floats
+//     (out-of-grid cells read as occupied; order z, then y, then x, each -1..1),
+//     then the goal delta (goal - agent) / 15 per axis: OBS_DIM = 30;
+//   - reward -0.01 per step, -0.1 on a blocked move, +1 on reaching the goal;
+//   - the episode ends at the goal or after 256 steps.
+//
+// RNG use per reset: 256 draws fill the grid (each 32-bit draw gives 16 cells,
+// a cell is occupied when its 2-bit field is 3), then rejection draws
+// (rngNext & 4095) for the agent cell and then the goal cell, at most 64 each;
+// if all 64 land on occupied cells the last drawn cell is cleared.
+//
+// The state is 4 KB per env, so the rollout kernels update it in place in
+// device memory instead of holding it in registers.
+#pragma once
+#include "../env.h"
+
+struct VoxelNav16 {
+    static constexpr int G = 16;
+    static constexpr int CELLS = G * G * G;
+    struct State {
+        int32_t px, py, pz;
+        int32_t gx, gy, gz;
+        uint32_t steps;
+        uint32_t pad;
+        uint8_t grid[CELLS];  // index (z * 16 + y) * 16 + x
+    };
+    using Action = int;
+    struct Obs {
+        float cells[27];
+        float goal[3];
+    };
+
+    static constexpr uint32_t OBS_DIM = 30;
+    static constexpr uint32_t ACT_DIM = 6;
+    static constexpr const char* KERNEL = "rollout_voxelnav16";
+    static constexpr uint32_t MAX_STEPS = 256;
+    static constexpr int MAX_TRIES = 64;
+
+    MG_HD static int cell(int x, int y, int z) { return (z * G + y) * G + x; }
+
+    MG_HD static bool occupied(const State& s, int x, int y, int z) {
+        if (x < 0 || y < 0 || z < 0 || x >= G || y >= G || z >= G) return true;
+        return s.grid[cell(x, y, z)] != 0;
+    }
+
+    MG_HD static int draw_free_cell(State& s, uint32_t& rng, int avoid) {
+        int c = 0;
+        for (int t = 0; t < MAX_TRIES; ++t) {
+            c = (int)(rngNext(rng) & (uint32_t)(CELLS - 1));
+            if (s.grid[c] == 0 && c != avoid) return c;
+        }
+        if (c == avoid) c = (c + 1) & (CELLS - 1);
+        s.grid[c] = 0;
+        return c;
+    }
+
+    MG_HD static void reset(State& s, uint32_t& rng) {
+        for (int w = 0; w < CELLS / 16; ++w) {
+            uint32_t r = rngNext(rng);
+            uint32_t packed[4];
+            for (int q = 0; q < 4; ++q) {
+                uint32_t word = 0;
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t f = (r >> (2 * (4 * q + j))) & 3u;
+                    word |= (uint32_t)(f == 3u) << (8 * j);
+                }
+                packed[q] = word;
+            }
+            __builtin_memcpy(s.grid + 16 * w, packed, 16);
+        }
+        int a = draw_free_cell(s, rng, -1);
+        int g = draw_free_cell(s, rng, a);
+        s.px = a % G;
+        s.py = (a / G) % G;
+        s.pz = a / (G * G);
+        s.gx = g % G;
+        s.gy = (g / G) % G;
+        s.gz = g / (G * G);
+        s.steps = 0;
+    }
+
+    MG_HD static void observe(const State& s, Obs& obs) {
+        int k = 0;
+        for (int dz = -1; dz <= 1; ++dz)
+            for (int dy = -1; dy <= 1; ++dy)
+                for (int dx = -1; dx <= 1; ++dx)
+                    obs.cells[k++] = occupied(s, s.px + dx, s.py + dy, s.pz + dz) ? 1.0f : 0.0f;
+        obs.goal[0] = (float)(s.gx - s.px) / 15.0f;
+        obs.goal[1] = (float)(s.gy - s.py) / 15.0f;
+        obs.goal[2] = (float)(s.gz - s.pz) / 15.0f;
+    }
+
+    MG_HD static void step(State& s, Action action, Obs& obs, float& reward, uint8_t& done) {
+        int a = action < 0 ? 0 : (action > 5 ? 5 : action);
+        int sign = (a & 1) ? -1 : 1;
+        int axis = a >> 1;
+        int nx = s.px + (axis == 0 ? sign : 0);
+        int ny = s.py + (axis == 1 ? sign : 0);
+        int nz = s.pz + (axis == 2 ? sign : 0);
+        bool blocked = occupied(s, nx, ny, nz);
+        if (!blocked) {
+            s.px = nx;
+            s.py = ny;
+            s.pz = nz;
+        }
+        s.steps += 1;
+        bool atGoal = s.px == s.gx && s.py == s.gy && s.pz == s.gz;
+        reward = atGoal ? 1.0f : (blocked ? -0.1f : -0.01f);
+        done = (atGoal || s.steps >= MAX_STEPS) ? 1 : 0;
+        observe(s, obs);
+    }
+};

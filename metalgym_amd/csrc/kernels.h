@@ -1,0 +1,58 @@
+// Launchers of the library's env-agnostic kernels (policy_kernels.hip,
+// train_kernels.hip). Each returns MG_OK or an MG_ERR_* code with the error set.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "internal.h"
+
+namespace mg {
+
+int launch_forward(hipStream_t st, const mg_policy_view& pv, const float* obs, uint32_t rows, float* head);
+int launch_sample(hipStream_t st, const mg_policy_view& pv, const float* head, uint32_t rows, uint32_t* rng,
+                  void* actions, float* logp, float* value);
+int launch_gae(hipStream_t st, const float* reward, const uint8_t* done, const float* value, const float* head,
+               uint32_t head_dim, uint32_t act_dim, uint32_t n, uint32_t horizon, float gamma, float lambda,
+               float* adv, float* ret);
+// Mean and 1 / (population std + 1e-8) of each minibatch block of the
+// advantage slots (model/gae.metal:42-77), [blocks][2].
+int launch_adv_stats(hipStream_t st, const float* adv, uint32_t n, uint32_t horizon, uint32_t minibatch,
+                     float* stats);
+
+// Everything one PPO minibatch update needs on the device.
+struct TrainWs {
+    float* xn;        // [(L+1)][B][128] normalised LN inputs
+    float* x;         // [(L+1)][B][128] LN outputs
+    float* sd;        // [(L+1)][B] LN standard deviations
+    float* v;         // [L][B][H] relu'd hidden activations
+    float* dxl;       // [(L+1)][B][128] gradients at the LN outputs
+    float* dhb;       // [L][B][128] gradients at the block outputs
+    float* dvb;       // [L][B][H] masked hidden gradients
+    float* dh0;       // [B][128] gradient at the embed output
+    float* dhead;     // [B][HD]
+    float* rowstats;  // [B][5]
+    float* dls;       // [B][A] per-row log_std gradients (Gaussian head)
+    float* partial;   // [kSplits][count] per-split weight-gradient partial sums
+    float* grad;      // [count] the reduced gradient (pre-clip)
+    float* normpart;  // [reduce blocks]
+    float* normsq;    // [1]
+    unsigned* counter;  // [1] last-block ticket
+};
+constexpr int kSplits = 16;  // row splits of the weight-gradient reductions
+
+struct TrainStep {
+    uint32_t row0;       // first slot row of the minibatch (t * n + r0)
+    uint32_t block;      // minibatch block id (index into adv stats)
+    uint32_t rows;       // B
+    uint32_t mb_index;   // index into the per-minibatch stats output
+    float beta1_pow, beta2_pow;
+};
+
+int train_ws_bytes(const mg_policy_view& pv, uint32_t rows, size_t* bytes);
+int train_ws_bind(const mg_policy_view& pv, uint32_t rows, void* base, TrainWs* ws);
+// One minibatch: rows pass, weight-gradient pass, reduce + norm, Adam.
+int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hparams& hp, float lr,
+                      const TrainWs& ws, const TrainStep& step, const float* obs_slots, const void* action_slots,
+                      const float* adv_slots, const float* ret_slots, const float* logp_slots,
+                      const float* adv_stats, float* m, float* v, float* head_out, float* mb_stats);
+
+}  // namespace mg

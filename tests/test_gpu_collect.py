@@ -1,0 +1,105 @@
+"""collect() on the GPU against the oracle, teacher-forced per step: the
+oracle replays every env with the GPU's actions, so RNG streams, env state,
+resets and done flags must match bit for bit, the policy head and values to
+1e-4, and GAE bit for bit on the GPU's own inputs (model/ppo.h:716-751)."""
+import numpy as np
+import pytest
+
+from parity import ENVS, THREADS, TOL_HEAD, assert_bit_exact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def run_collect_parity(mg, orc, env, n, T, layers=2, scale=4, seed=0, collects=2):
+    eid, kernel = ENVS[env]
+    gym = mg.Gym(kernel, n, seed)
+    model = mg.PPOModel(gym, scale=scale, layers=layers, horizon=T, seed=seed)
+    d = orc.dims(eid, hidden=128 * scale, layers=layers)
+    params = orc.init_params(d, seed)
+    assert_bit_exact(model.params(), params, "initial parameters")
+    g = orc.GymState(eid, n, seed)
+    slots = orc.Slots(eid, n, T)
+    for c in range(collects):
+        model.collect()
+        s = model.download_slots()
+        head = model.head()
+        sampled = orc.collect(g, d, params, T, slots, first=(c == 0), teacher_actions=s["actions"],
+                              threads=THREADS)
+        tag = f"{env} collect {c}"
+        # env side: bit-exact under teacher forcing
+        assert_bit_exact(s["obs"], slots.obs, f"{tag} obs slots")
+        assert_bit_exact(s["reward"], slots.reward, f"{tag} rewards")
+        assert_bit_exact(s["done"], slots.done, f"{tag} dones")
+        assert_bit_exact(gym.rng(), g.rng, f"{tag} rng")
+        assert_bit_exact(gym.state(), g.state, f"{tag} state")
+        assert_bit_exact(gym.done(), g.done, f"{tag} live done")
+        # policy side: within 1e-4
+        assert_close(s["value"], slots.value, TOL_HEAD, f"{tag} values")
+        assert_close(s["logp"], slots.logp, TOL_HEAD, f"{tag} logp")
+        assert_close(head, slots.head, TOL_HEAD, f"{tag} bootstrap head")
+        if gym.continuous:
+            assert_close(s["actions"], sampled, TOL_HEAD, f"{tag} gaussian samples")
+        else:
+            flips = int((s["actions"] != sampled).sum())
+            assert flips <= max(2, s["actions"].size // 10000), f"{tag}: {flips} sampled actions differ"
+        # GAE: bit-exact on the GPU's own inputs, 1e-4 against the oracle's
+        adv, ret = orc.gae(s["reward"], s["done"], s["value"], head, gym.act_dim)
+        assert_bit_exact(s["adv"], adv, f"{tag} advantages")
+        assert_bit_exact(s["ret"], ret, f"{tag} returns")
+        assert_close(s["adv"], slots.adv, TOL_HEAD, f"{tag} advantages vs oracle")
+    return model, s
+
+
+@pytest.mark.parametrize("env,n,T", [
+    ("cartpole", 4096, 8),
+    ("cartpole", 64 * 576, 2),   # 64-row tiles (n >= 64 * 512)
+    ("cartpole_continuous", 2048, 8),
+    ("voxelnav16", 1024, 8),
+])
+def test_collect_teacher_forced(mg, orc, env, n, T):
+    run_collect_parity(mg, orc, env, n, T)
+
+
+@pytest.mark.parametrize("layers,scale", [(1, 1), (3, 2)])
+def test_collect_other_shapes(mg, orc, layers, scale):
+    run_collect_parity(mg, orc, "cartpole", 1024, 4, layers=layers, scale=scale, seed=11, collects=1)
+
+
+@pytest.mark.parametrize("env", ["cartpole", "voxelnav16", "cartpole_continuous"])
+def test_forward_matches_oracle(mg, orc, env):
+    """forward() (model/ppo.h:628-634) on arbitrary rows, including a ragged count."""
+    eid, kernel = ENVS[env]
+    gym = mg.Gym(kernel, 256, 0)
+    model = mg.PPOModel(gym, horizon=4)
+    d = orc.dims(eid)
+    rs = np.random.default_rng(3)
+    obs = (rs.standard_normal((1000, gym.obs_dim)) * 3).astype(np.float32)
+    head = model.forward(obs)
+    want = orc.forward(d, model.params(), obs, threads=THREADS)
+    assert_close(head, want, TOL_HEAD, "head")
+
+
+@pytest.mark.parametrize("env", ["cartpole", "voxelnav16", "cartpole_continuous"])
+def test_sampler_matches_oracle(mg, orc, env):
+    """Sampling alone on a given head: actions and RNG bit-exact, logp to 1e-4."""
+    import ctypes as C
+
+    eid, kernel = ENVS[env]
+    gym = mg.Gym(kernel, 256, 0)
+    model = mg.PPOModel(gym, horizon=4)
+    d = orc.dims(eid)
+    rs = np.random.default_rng(4)
+    rows = 4096
+    head = rs.standard_normal((rows, gym.act_dim + 1)).astype(np.float32)
+    rng = rs.integers(1, 2**32 - 1, rows, dtype=np.uint32)
+    a, lp, v, r2 = model.sample(head, rng)
+    oa = np.zeros(gym.action_shape(rows), gym.action_dtype)
+    olp = np.zeros(rows, np.float32)
+    ov = np.zeros(rows, np.float32)
+    orng = rng.copy()
+    orc.lib().orc_sample(C.byref(d), orc.ptr(model.params()), orc.ptr(head), rows, orc.ptr(orng), orc.ptr(oa),
+                         orc.ptr(olp), orc.ptr(ov))
+    assert_bit_exact(r2, orng, "rng")
+    assert_bit_exact(a, oa, "actions")
+    assert_bit_exact(lp, olp, "logp")
+    assert_bit_exact(v, ov, "value")

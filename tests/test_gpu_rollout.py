@@ -1,0 +1,92 @@
+"""rollout<Env> on the GPU against the oracle: RNG streams, env state, resets,
+done flags, observations and rewards must be bit-exact (rollout.h:31-54)."""
+import numpy as np
+import pytest
+
+from parity import ENVS, THREADS, assert_bit_exact
+
+pytestmark = pytest.mark.gpu
+
+
+def compare_gym(gym, g, what):
+    assert_bit_exact(gym.state(), g.state, f"{what} state")
+    assert_bit_exact(gym.rng(), g.rng, f"{what} rng")
+    assert_bit_exact(gym.done(), g.done, f"{what} done")
+
+
+@pytest.mark.parametrize("env,n,steps,seed", [
+    ("cartpole", 4096, 32, 0),
+    ("cartpole", 1000, 600, 3),           # ragged n; long enough for truncation at 500
+    ("cartpole_continuous", 2048, 64, 0),
+    ("cartpole_continuous_clamp", 2048, 64, 1),
+    ("voxelnav16", 512, 300, 0),          # past the 256-step cap
+])
+def test_random_rollout_bit_exact(mg, orc, env, n, steps, seed):
+    eid, kernel = ENVS[env]
+    gym = mg.Gym(kernel, n, seed)
+    g = orc.GymState(eid, n, seed)
+    compare_gym(gym, g, "init")
+    for rep in range(2):  # state carries over between launches
+        bufs = gym.rollout_random(steps)
+        acts, obs, rew, dn = gym.download_slots(bufs, steps)
+        oa, oo, orw, od = orc.rollout(g, steps, random=True, threads=THREADS)
+        assert_bit_exact(acts, oa, f"{env} rep {rep} actions")
+        assert_bit_exact(obs, oo, f"{env} rep {rep} obs")
+        assert_bit_exact(rew, orw, f"{env} rep {rep} reward")
+        assert_bit_exact(dn, od, f"{env} rep {rep} done slots")
+        compare_gym(gym, g, f"{env} rep {rep}")
+    assert dn.any(), "no episode ended: the test does not exercise resets"
+
+
+@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "voxelnav16"])
+def test_given_action_rollout_bit_exact(mg, orc, env):
+    eid, kernel = ENVS[env]
+    n, steps = 2048, 40
+    gym = mg.Gym(kernel, n, 5)
+    g = orc.GymState(eid, n, 5)
+    rs = np.random.default_rng(1)
+    if gym.continuous:
+        acts = (rs.standard_normal((steps, n, gym.act_dim)) * 2).astype(np.float32)
+    else:
+        acts = rs.integers(0, gym.act_dim, (steps, n)).astype(np.int32)
+    bufs = gym.rollout_given(steps, acts)
+    _, obs, rew, dn = gym.download_slots(bufs, steps)
+    _, oo, orw, od = orc.rollout(g, steps, random=False, actions_in=acts, threads=THREADS)
+    assert_bit_exact(obs, oo, "obs")
+    assert_bit_exact(rew, orw, "reward")
+    assert_bit_exact(dn, od, "done")
+    compare_gym(gym, g, env)
+
+
+def test_gym_run_single_steps(mg, orc):
+    """gym.run() (gym.h:110-121): one step from the action buffer into obs/reward."""
+    n = 640
+    gym = mg.Gym("rollout_cartpole", n, 0)
+    g = orc.GymState(0, n, 0)
+    rs = np.random.default_rng(2)
+    for _ in range(30):
+        a = rs.integers(0, 2, n).astype(np.int32)
+        gym.set_actions(a)
+        gym.run()
+        _, oo, orw, _ = orc.rollout(g, 1, random=False, actions_in=a[None], threads=THREADS)
+        assert_bit_exact(gym.obs(), oo[0], "obs")
+        assert_bit_exact(gym.reward(), orw[0], "reward")
+    compare_gym(gym, g, "run")
+
+
+def test_large_random_rollout_invariants(mg):
+    """At the benchmark size, size-independent properties: rewards are 1,
+    RNG states never hit the absorbing 0, every done flag matches a threshold
+    crossing or the 500-step cap, and obs stay inside the reset box after a reset."""
+    n, steps = 262144, 32
+    gym = mg.Gym("rollout_cartpole", n, 0)
+    bufs = gym.rollout_random(steps)
+    acts, obs, rew, dn = gym.download_slots(bufs, steps)
+    assert np.all(rew == 1.0)
+    assert np.all((acts == 0) | (acts == 1))
+    assert np.all(gym.rng() != 0)
+    theta_thr = np.float32(12.0 * 2.0 * np.float32(np.pi) / 360.0)
+    term = (np.abs(obs[..., 0]) > 2.4) | (np.abs(obs[..., 2]) > theta_thr)
+    assert np.array_equal(dn.astype(bool), term)  # no truncation within 32 steps of a fresh start
+    # each env's actions are roughly fair coin flips
+    assert abs(acts.mean() - 0.5) < 0.01

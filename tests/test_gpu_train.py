@@ -1,0 +1,142 @@
+"""PPO training on the GPU against the oracle (model/ppo.h:906-943): one
+minibatch and short multi-minibatch runs on the GPU's own rollout, comparing
+the recomputed head (1e-4), the Adam first moment (a scaled copy of the
+clipped gradient), LossStats and the post-Adam weights (1e-3)."""
+import numpy as np
+import pytest
+
+from parity import ENVS, THREADS, TOL_HEAD, TOL_TRAIN, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def setup(mg, orc, env, n, T, B, seed=0, layers=2, scale=4):
+    eid, kernel = ENVS[env]
+    gym = mg.Gym(kernel, n, seed)
+    model = mg.PPOModel(gym, scale=scale, layers=layers, horizon=T, seed=seed, minibatch=B)
+    d = orc.dims(eid, hidden=128 * scale, layers=layers)
+    model.collect()
+    return gym, model, d
+
+
+def block_rows(s, n, B, block):
+    per = n // B
+    t, r0 = block // per, (block % per) * B
+    sl = slice(r0, r0 + B)
+    return (s["obs"][t, sl], s["actions"][t, sl], s["adv"][t, sl], s["ret"][t, sl], s["logp"][t, sl])
+
+
+def group_errors(pv, a, b):
+    """Relative L2 error per parameter group (canonical layout offsets)."""
+    L, E, H, HD = pv.layers, pv.embed, pv.hidden, pv.head_dim
+    groups = {"in_w": (pv.off_in_w, pv.obs_dim * E), "in_b": (pv.off_in_b, E), "head": (pv.off_head, E * HD)}
+    for l in range(L + 1):
+        groups[f"ln{l}_gamma"] = (pv.off_ln_gamma[l], E)
+        groups[f"ln{l}_beta"] = (pv.off_ln_beta[l], E)
+    for l in range(L):
+        groups[f"up{l}"] = (pv.off_up[l], E * H)
+        groups[f"down{l}"] = (pv.off_down[l], H * E)
+    if pv.continuous:
+        groups["log_std"] = (pv.off_log_std, pv.act_dim)
+    out = {}
+    for k, (o, c) in groups.items():
+        x, y = a[o:o + c].astype(np.float64), b[o:o + c].astype(np.float64)
+        out[k] = float(np.linalg.norm(x - y) / max(np.linalg.norm(y), 1e-30))
+    return out
+
+
+def compare_moments(pv, m_gpu, m_orc, what):
+    """The first Adam moment is 0.1 x the clipped gradient. Weight-gradient sums
+    over thousands of rows in a different fp32 order differ at the 1e-5..1e-4
+    relative level; a wrong term shows up as O(1)."""
+    errs = group_errors(pv, m_gpu, m_orc)
+    worst = max(errs, key=errs.get)
+    assert errs[worst] < 1e-3, f"{what}: relative L2 error {errs[worst]:.3g} in {worst}; all: {errs}"
+
+
+@pytest.mark.parametrize("env,n,T,B,block", [
+    ("cartpole", 4096, 2, 4096, 1),
+    ("cartpole", 2048, 2, 512, 5),
+    ("cartpole", 1280, 2, 320, 3),      # minibatch not a multiple of 128
+    ("cartpole_continuous", 2048, 2, 1024, 2),
+    ("voxelnav16", 1024, 2, 512, 1),
+])
+def test_one_minibatch(mg, orc, env, n, T, B, block):
+    gym, model, d = setup(mg, orc, env, n, T, B)
+    s = model.download_slots()
+    p0 = model.params()
+    hp = orc.hparams()
+    model.train_block(block)
+    p1 = model.params()
+    m1, v1, step = model.adam_state()
+    assert step == 1
+    P, M, V = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    st, grad, head = orc.train_minibatch(d, hp, P, M, V, 1, *block_rows(s, n, B, block), threads=THREADS)
+    assert_close(model.head(), head, TOL_HEAD, "recomputed head")
+    compare_moments(model.pv, m1, M, "first moment (clipped gradient)")
+    print("gradient relative errors per group:", group_errors(model.pv, m1, M))
+    assert_close(p1, P, TOL_TRAIN, "post-Adam weights")
+    got, want = np.array(model.last_stats().as_tuple()), np.array(st.as_tuple())
+    assert_close(got[[0, 1, 2, 3, 5]], want[[0, 1, 2, 3, 5]], TOL_TRAIN, "LossStats")
+    assert abs(got[4] - want[4]) * B <= 2.0 + 1e-3, (got[4], want[4])
+    assert np.all(np.isfinite(p1))
+
+
+@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous"])
+def test_train_epochs(mg, orc, env):
+    """train(2) over 2 slots x 2 blocks: the block order and every minibatch's
+    LossStats match the oracle's train loop; weights stay within 1e-3."""
+    n, T, B = 1024, 2, 512
+    eid, _ = ENVS[env]
+    gym, model, d = setup(mg, orc, env, n, T, B, seed=7)
+    s = model.download_slots()
+    p0 = model.params()
+    model.train(2)
+    stats = model.train_stats()
+    order = model.last_order()
+    P, M, V = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    import ctypes as C
+
+    step = C.c_uint32(0)
+    shuf = C.c_uint64(0)
+    orc.lib().orc_shuffle_state_init(7, C.byref(shuf))
+    blocks = T * (n // B)
+    order_state = np.arange(blocks, dtype=np.uint32)
+    ost = (orc.Stats * (2 * blocks))()
+    acts = np.ascontiguousarray(s["actions"])
+    orc.lib().orc_train(C.byref(d), C.byref(orc.hparams()), orc.ptr(P), orc.ptr(M), orc.ptr(V), C.byref(step),
+                        C.byref(shuf), n, T, B, 2, orc.ptr(np.ascontiguousarray(s["obs"])), orc.ptr(acts),
+                        orc.ptr(np.ascontiguousarray(s["adv"])), orc.ptr(np.ascontiguousarray(s["ret"])),
+                        orc.ptr(np.ascontiguousarray(s["logp"])), ost, orc.ptr(order_state), THREADS)
+    # replay the oracle's order
+    shuf2 = C.c_uint64(0)
+    orc.lib().orc_shuffle_state_init(7, C.byref(shuf2))
+    o = np.arange(blocks, dtype=np.uint32)
+    want = []
+    for _ in range(2):
+        orc.lib().orc_shuffle_blocks(C.byref(shuf2), orc.ptr(o), blocks)
+        want += list(o)
+    assert list(order) == want
+    assert step.value == 2 * blocks
+    ostats = np.array([ost[i].as_tuple() for i in range(2 * blocks)], np.float32)
+    # clip_frac counts rows with |ratio - 1| > clip: a row sitting on the clip
+    # boundary may land on either side, so it is compared in whole rows
+    cols = [0, 1, 2, 3, 5]
+    assert_close(stats[:, cols], ostats[:, cols], TOL_TRAIN, "per-minibatch LossStats")
+    assert np.all(np.abs(stats[:, 4] - ostats[:, 4]) * B <= 2.0 + 1e-3), (stats[:, 4], ostats[:, 4])
+    assert_close(model.params(), P, TOL_TRAIN, "weights after 2 epochs")
+
+
+def test_full_loop_learns(mg):
+    """A short CartPole run on the real path improves the mean episode length."""
+    gym = mg.Gym("rollout_cartpole", 4096, 0)
+    model = mg.PPOModel(gym, horizon=32)
+    lens = []
+    for it in range(12):
+        model.collect()
+        d = model.download_slots()["done"]
+        lens.append(d.size / max(1, d.sum()))
+        model.train(4)
+        st = model.last_stats()
+        assert np.all(np.isfinite(st.as_tuple()))
+    assert np.mean(lens[-3:]) > 1.5 * np.mean(lens[:3]), lens
