@@ -1,0 +1,230 @@
+"""Benchmark of the rollout-and-policy hot path on one MI355X.
+
+Headline: CartPole with policy, collect() at 262144 envs, T = 32, the 2-block
+residual MLP (embed 128, hidden 512) -- BASELINE.json config 2 at its largest
+size. One step = one collect() (262144 x 32 env steps, policy forward on fp32
+MFMA, sampling, env step, GAE). Inputs are synthetic (seeded envs and weights)
+and resident on the GPU. The other configurations (random policy, full PPO loop,
+continuous, VoxelNav16) are reported as extra fields of the same JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA = 157.3e12  # FLOP/s, MI355X dense fp32 matrix
+PEAK_HBM = 8.0e12          # B/s
+E, H, L = 128, 512, 2
+
+
+def fwd_flop(O, A, layers=L, hidden=H):
+    """Algorithmic FLOP of one policy forward row (embed, blocks, head)."""
+    return 2 * (O * E + 2 * layers * E * hidden + E * (A + 1))
+
+
+def bwd_flop(O, A, layers=L, hidden=H):
+    """dX chain + weight gradients of one row (no dX for the embed)."""
+    dx = 2 * (2 * layers * E * hidden + E * (A + 1))
+    dw = fwd_flop(O, A, layers, hidden)
+    return dx + dw
+
+
+def sync():
+    import metalgym_amd as mg
+
+    mg.lib().mg_synchronize()
+
+
+def kernel_avg_ms(times, k):
+    tot, cnt = times[k]
+    return tot / cnt if cnt else float("nan")
+
+
+def bench_collect(kernel, n, T, steps, warmup, O, A):
+    import metalgym_amd as mg
+
+    gym = mg.Gym(kernel, n, 0)
+    model = mg.PPOModel(gym, horizon=T)
+    for _ in range(warmup):
+        model.collect()
+    sync()
+    mg.timing_reset()
+    mg.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.collect()
+    sync()
+    dt = time.perf_counter() - t0
+    mg.timing_enable(False)
+    times = mg.timing_get()
+    return gym, model, dt, times
+
+
+def bench_random(n, T, reps):
+    import metalgym_amd as mg
+
+    gym = mg.Gym("rollout_cartpole", n, 0)
+    bufs = gym.rollout_random(T)
+    sync()
+    mg.timing_reset()
+    mg.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        gym.rollout_random(T, bufs, sync=False)
+    sync()
+    dt = time.perf_counter() - t0
+    mg.timing_enable(False)
+    times = mg.timing_get()
+    kms = kernel_avg_ms(times, "rollout")
+    bytes_launch = n * T * 25 + n * 2 * (20 + 4 + 1)
+    return {"env_steps_per_s": reps * n * T / dt, "kernel_us": kms * 1e3,
+            "hbm_GBps": bytes_launch / (kms * 1e-3) / 1e9, "hbm_frac": bytes_launch / (kms * 1e-3) / PEAK_HBM}
+
+
+def bench_full(kernel, n, T, iters, O, A, epochs=4):
+    import metalgym_amd as mg
+
+    gym = mg.Gym(kernel, n, 0)
+    model = mg.PPOModel(gym, horizon=T)
+    model.collect()
+    model.train(1)
+    sync()
+    mg.timing_reset()
+    mg.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        model.collect()
+        model.train(epochs)
+    sync()
+    dt = time.perf_counter() - t0
+    mg.timing_enable(False)
+    times = mg.timing_get()
+    st = model.last_stats()
+    B = min(n, 4096)
+    out = {"env_steps_per_s": iters * n * T / dt, "s_per_iter": dt / iters,
+           "minibatches_per_iter": epochs * T * n // B,
+           "last_stats": dict(zip(["policy", "value", "entropy", "approx_kl", "clip_frac", "grad_norm"],
+                                  [round(x, 6) for x in st.as_tuple()]))}
+    kern = {}
+    for k in ("collect", "gae", "adv_stats", "train_rows", "train_dw", "grad_reduce", "adam"):
+        kern[k + "_us"] = round(kernel_avg_ms(times, k) * 1e3, 2)
+    tr = kernel_avg_ms(times, "train_rows") * 1e-3
+    dw = kernel_avg_ms(times, "train_dw") * 1e-3
+    ad = kernel_avg_ms(times, "adam") * 1e-3
+    count = model.pv.count
+    kern["train_rows_TFLOPs"] = round(B * (fwd_flop(O, A) + bwd_flop(O, A) - fwd_flop(O, A)) / tr / 1e12, 2)
+    kern["train_dw_TFLOPs"] = round(B * fwd_flop(O, A) / dw / 1e12, 2)
+    kern["adam_GBps"] = round(count * 28 / ad / 1e9, 1)
+    out["kernels"] = kern
+    return out
+
+
+def cpu_baseline(target_s=10.0):
+    """The CPU oracle's collect() on a bounded slice of the headline workload
+    (CartPole, T = 32, same network), on the host's cores."""
+    import numpy as np
+
+    import oracle as orc
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    T = 32
+    d = orc.dims(orc.CARTPOLE)
+    params = orc.init_params(d, 0)
+
+    def run(n):
+        g = orc.GymState(orc.CARTPOLE, n, 0)
+        s = orc.Slots(orc.CARTPOLE, n, T)
+        t0 = time.perf_counter()
+        orc.collect(g, d, params, T, s, first=True, threads=threads)
+        return time.perf_counter() - t0
+
+    n = 64 * threads
+    dt = run(n)
+    n = int(max(64, min(262144, n * target_s / max(dt, 1e-3))) // 64 * 64)
+    dt = run(n)
+    return {"value": n * T / dt, "unit": "env steps/s", "cores": threads, "kind": "port",
+            "sample": f"oracle collect() of {n} of the 262144 CartPole envs, T=32, 2-block MLP, fp32, "
+                      f"{threads} threads, {dt:.1f} s"}
+
+
+def pmc_traffic():
+    """HBM bytes per collect launch from the committed rocprofv3 --pmc summary, if any."""
+    p = os.path.join(ROOT, "profiles", "collect_cartpole_262144_pmc.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X; this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import metalgym_amd as mg
+
+    n, T = 262144, 32
+    O, A = 4, 2
+    gym, model, dt, times = bench_collect("rollout_cartpole", n, T, args.steps, args.warmup, O, A)
+    value = args.steps * n * T / dt
+    kms = kernel_avg_ms(times, "collect")
+    flop_launch = (T + 1) * n * fwd_flop(O, A)
+    achieved = flop_launch / (kms * 1e-3)
+    gae_ms = kernel_avg_ms(times, "gae")
+    line = {
+        "metric": "CartPole env steps/s: random, w/ policy, full PPO loop @4096 & 262144 envs",
+        "value": value,
+        "unit": "env steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded envs and weights)",
+        "config": {"workload": "cartpole_collect_with_policy", "envs": n, "horizon": T, "embed": E, "hidden": H,
+                   "layers": L, "head": "softmax(2)+value", "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "kernel": "collect_kernel<CartPole,64>", "achieved": achieved / 1e12,
+                     "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
+                     "traffic": pmc_traffic(), "flop_per_launch": flop_launch, "kernel_ms": kms},
+        "gae": {"kernel_us": gae_ms * 1e3, "hbm_GBps": (n * T * 17 + n * 4) / (gae_ms * 1e-3) / 1e9},
+    }
+    del model, gym
+    if not args.no_extra:
+        extra = {}
+        extra["random_4096"] = bench_random(4096, 32, 50)
+        extra["random_262144"] = bench_random(262144, 32, 20)
+        _, _, dt4, t4 = bench_collect("rollout_cartpole", 4096, 32, 20, 2, O, A)
+        extra["collect_4096"] = {"env_steps_per_s": 20 * 4096 * 32 / dt4,
+                                 "vs_published_m4_3.8M": 20 * 4096 * 32 / dt4 / 3.8e6}
+        extra["full_ppo_4096"] = bench_full("rollout_cartpole", 4096, 32, 5, O, A)
+        extra["full_ppo_4096"]["vs_published_m4_296K"] = extra["full_ppo_4096"]["env_steps_per_s"] / 296e3
+        extra["full_ppo_262144"] = bench_full("rollout_cartpole", 262144, 32, 1, O, A)
+        _, _, dtc, _ = bench_collect("rollout_cartpole_continuous", 262144, 32, 3, 1, 4, 1)
+        extra["continuous_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtc}
+        _, _, dtv, tv = bench_collect("rollout_voxelnav16", 262144, 32, 3, 1, 30, 6)
+        extra["voxelnav16_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtv,
+                                              "collect_ms": kernel_avg_ms(tv, "collect")}
+        line["extra"] = extra
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

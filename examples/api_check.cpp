@@ -1,0 +1,93 @@
+// End-to-end check of the C++ API surface (Gym<Env>, PPOModel<Env>) on the
+// GPU: every public call of the reference's API runs once and its result is
+// checked for the invariants the reference documents (README.md:100-156).
+#include <cmath>
+#include <cstdio>
+#include <random>
+
+#include "mg/envs/cartpole.h"
+#include "mg/envs/cartpole_continuous.h"
+#include "mg/ppo.h"
+
+static int failures = 0;
+#define CHECK(cond)                                                        \
+    do {                                                                   \
+        if (!(cond)) {                                                     \
+            std::printf("FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond); \
+            ++failures;                                                    \
+        }                                                                  \
+    } while (0)
+
+int main() {
+    const uint32_t N = 256, T = 8;
+    {
+        Gym<CartPole> gym(N);
+        const uint8_t* d0 = gym.done();
+        for (uint32_t i = 0; i < N; i++) CHECK(d0[i] == 1);  // gym.h:54-55
+        std::vector<float> reward(N, 0.0f);
+        for (uint32_t i = 0; i < N; i++) gym.actions()[i] = (int)(i & 1);
+        gym.run(reward);
+        const CartPole::Obs* o = gym.obs();
+        for (uint32_t i = 0; i < N; i++) {
+            CHECK(reward[i] == 1.0f);
+            CHECK(std::fabs(o[i].x) < 0.06f && std::fabs(o[i].theta) < 0.06f);
+        }
+        PPOModel<CartPole> model(gym, 128, 4, 2, 3e-4f, T);
+        CHECK(model.minibatchRows() == N);
+        model.collect();
+        for (uint32_t t = 0; t < T; t++) {
+            for (uint32_t i = 0; i < N; i++) {
+                CHECK(model.slotRewards(t)[i] == 1.0f);
+                CHECK(model.slotActions(t)[i] == 0 || model.slotActions(t)[i] == 1);
+                CHECK(model.slotReturns(t)[i] == model.slotAdvantages(t)[i] + model.slotValues(t)[i]);
+                CHECK(std::isfinite(model.slotValues(t)[i]));
+            }
+        }
+        // bootstrap value = head column ACT_DIM of the last forward (model/gae.metal:27)
+        const float vT = model.headValue(0, CartPole::ACT_DIM);
+        CHECK(model.slotReturns(T - 1)[0] == model.slotAdvantages(T - 1)[0] + model.slotValues(T - 1)[0]);
+        CHECK(std::isfinite(vT));
+        model.forward();
+        std::mt19937 rng(1);
+        model.act(rng);
+        for (uint32_t i = 0; i < N; i++) {
+            CHECK(gym.actions()[i] == 0 || gym.actions()[i] == 1);
+            CHECK(model.values()[i] == model.headValue(i, CartPole::ACT_DIM));
+            CHECK(model.logProbs()[i] < 0.0f);
+        }
+        model.actGreedy();
+        for (uint32_t i = 0; i < N; i++) {
+            const int best = model.headValue(i, 1) > model.headValue(i, 0) ? 1 : 0;
+            CHECK(gym.actions()[i] == best);
+        }
+        model.train(1);
+        LossStats s = model.lastStats();
+        CHECK(std::isfinite(s.policy) && std::isfinite(s.value) && s.gradNorm > 0.0f);
+        CHECK(s.entropy > 0.6f && s.entropy <= 0.6932f);
+        CHECK(model.trainStats().size() == T);
+        model.trainSlot(3);
+        CHECK(model.trainStats().size() == 1);
+        model.clip = 0.1f;
+        model.collect();
+        model.train(1);
+        CHECK(std::isfinite(model.lastStats().gradNorm));
+    }
+    {
+        Gym<CartPoleContinuous> gym(N);
+        PPOModel<CartPoleContinuous> model(gym, 128, 4, 2, 3e-4f, T);
+        CHECK(model.logStdValue(0) == 0.0f);  // model/ppo.h:115
+        model.setLogStd(-0.5f);
+        CHECK(model.logStdValue(0) == -0.5f);
+        model.collect();
+        model.train(1);
+        LossStats s = model.lastStats();
+        CHECK(std::isfinite(s.policy) && s.gradNorm > 0.0f);
+        CHECK(model.logStdValue(0) != -0.5f);  // Adam moved it
+        std::mt19937 rng(2);
+        model.forward();
+        model.act(rng);
+        CHECK(std::isfinite(gym.actions()[0].force));
+    }
+    std::printf(failures ? "api_check FAILED (%d)\n" : "api_check ok\n", failures);
+    return failures ? 1 : 0;
+}

@@ -265,6 +265,8 @@ int mg_ppo_check_config(const char* kernel, uint32_t n, const mg_ppo_config* con
  * before it. */
 int mg_ppo_create(mg_gym* gym, const mg_ppo_config* config, mg_ppo** out);
 int mg_ppo_destroy(mg_ppo* model);
+/* The effective configuration (minibatch resolved from 0 to its default). */
+int mg_ppo_config_get(mg_ppo* model, mg_ppo_config* out);
 int mg_ppo_set_hparams(mg_ppo* model, const mg_ppo_hparams* hp);
 int mg_ppo_get_hparams(mg_ppo* model, mg_ppo_hparams* hp);
 /* model/ppo.h:716-751: one rollout of T steps plus GAE. Blocking. */

@@ -122,6 +122,7 @@ def lib():
         "mg_ppo_check_config": (I, [C.c_char_p, u32, P]),
         "mg_ppo_create": (I, [P, P, P]),
         "mg_ppo_destroy": (I, [P]),
+        "mg_ppo_config_get": (I, [P, P]),
         "mg_ppo_set_hparams": (I, [P, P]),
         "mg_ppo_get_hparams": (I, [P, P]),
         "mg_ppo_collect": (I, [P]),

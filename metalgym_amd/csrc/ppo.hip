@@ -315,6 +315,12 @@ int mg_ppo_destroy(mg_ppo* p) {
     return MG_OK;
 }
 
+int mg_ppo_config_get(mg_ppo* p, mg_ppo_config* out) {
+    MG_CHECK(p && out, MG_ERR_INVALID, "config_get: null argument");
+    *out = p->cfg;
+    return MG_OK;
+}
+
 int mg_ppo_set_hparams(mg_ppo* p, const mg_ppo_hparams* hp) {
     MG_CHECK(p && hp, MG_ERR_INVALID, "mg_ppo_set_hparams: null argument");
     p->hp = *hp;

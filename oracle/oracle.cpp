@@ -814,8 +814,11 @@ void orc_train_minibatch(const orc_dims* dp, const orc_hparams* hp, float* P, fl
     if (grad_out) std::memcpy(grad_out, g.data(), (size_t)L.count * 4);
 
     // model/optimizer.metal:23-60 with the host step of model/ppo.h:873-881
-    float normSq = 0.0f;
-    for (uint32_t i = 0; i < L.count; ++i) normSq += g[i] * g[i];
+    // The reference adds per-SIMD partial squares with float atomics in an
+    // unspecified order; the checker accumulates in double, then rounds once.
+    double normSqD = 0.0;
+    for (uint32_t i = 0; i < L.count; ++i) normSqD += (double)g[i] * (double)g[i];
+    float normSq = (float)normSqD;
     const float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f;
     float b1p = std::pow(beta1, (float)step), b2p = std::pow(beta2, (float)step);
     float norm = std::sqrt(normSq);

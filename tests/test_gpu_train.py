@@ -46,12 +46,37 @@ def group_errors(pv, a, b):
 
 
 def compare_moments(pv, m_gpu, m_orc, what):
-    """The first Adam moment is 0.1 x the clipped gradient. Weight-gradient sums
-    over thousands of rows in a different fp32 order differ at the 1e-5..1e-4
-    relative level; a wrong term shows up as O(1)."""
+    """The first Adam moment is 0.1 x the clipped gradient. fp32 sums in a
+    different order differ by 1e-6 near the head and up to ~1e-4 in the first
+    block (LayerNorm backward cancels most of its input); a wrong term is O(1)."""
     errs = group_errors(pv, m_gpu, m_orc)
     worst = max(errs, key=errs.get)
     assert errs[worst] < 1e-3, f"{what}: relative L2 error {errs[worst]:.3g} in {worst}; all: {errs}"
+
+
+def float64_moment(pv, params, rows, hp):
+    """0.1 x the clipped gradient of the minibatch loss in float64, from the torch
+    restatement that generates the golden fixtures (tests/golden/make_golden.py)."""
+    import torch
+
+    from golden import make_golden as mk
+
+    O, A, E, H, L, cont = pv.obs_dim, pv.act_dim, pv.embed, pv.hidden, pv.layers, bool(pv.continuous)
+    obs, acts, adv, ret, old = rows
+    t = mk.torch_params(params, O, A, E, H, L, cont)
+    head = mk.forward(t, torch.tensor(obs, dtype=torch.float64), E, L)
+    act_t = torch.tensor(acts, dtype=torch.float64 if cont else torch.int64)
+    f64 = lambda x: torch.tensor(x, dtype=torch.float64)
+    loss, _, _ = mk.ppo_loss(head, A, cont, t, act_t, f64(adv), f64(ret), f64(old), hp.clip, hp.value_coef,
+                             hp.entropy_coef)
+    loss.backward()
+    off, count = mk.layout(O, A, E, H, L, cont)
+    g = np.zeros(count)
+    for k, v in t.items():
+        g[off[k]:off[k] + v.numel()] = v.grad.numpy().ravel()
+    norm = np.linalg.norm(g)
+    scale = hp.max_grad_norm / (norm + 1e-6) if norm > hp.max_grad_norm else 1.0
+    return 0.1 * g * scale
 
 
 @pytest.mark.parametrize("env,n,T,B,block", [
@@ -74,7 +99,27 @@ def test_one_minibatch(mg, orc, env, n, T, B, block):
     st, grad, head = orc.train_minibatch(d, hp, P, M, V, 1, *block_rows(s, n, B, block), threads=THREADS)
     assert_close(model.head(), head, TOL_HEAD, "recomputed head")
     compare_moments(model.pv, m1, M, "first moment (clipped gradient)")
-    print("gradient relative errors per group:", group_errors(model.pv, m1, M))
+    # both fp32 gradients against the float64 one: the GPU is as close as the oracle
+    m64 = float64_moment(model.pv, p0, block_rows(s, n, B, block), hp)
+    e_gpu, e_orc = group_errors(model.pv, m1, m64), group_errors(model.pv, M, m64)
+    print("float64 gradient error per group, gpu:", e_gpu, "oracle:", e_orc)
+    # A hidden pre-activation within ~1e-6 of zero can fall on either side of the
+    # ReLU under a different fp32 summation order; that unit's gradient path then
+    # switches on or off. Its signature: one column of an up matrix holds almost
+    # all of that matrix's error (the error then spreads into the layers below).
+    pv = model.pv
+    flip = False
+    for l in range(pv.layers):
+        o = pv.off_up[l]
+        d = (m1[o:o + pv.embed * pv.hidden] - m64[o:o + pv.embed * pv.hidden]).reshape(pv.embed, pv.hidden)
+        col = (d.astype(np.float64) ** 2).sum(0)
+        share = col.max() / max(col.sum(), 1e-300)
+        print(f"up{l}: worst hidden column {col.argmax()} holds {share:.3f} of the squared error")
+        flip |= share > 0.9 and e_gpu[f"up{l}"] > 2e-5
+    for k in e_gpu:
+        assert e_gpu[k] < 1e-3, (k, e_gpu[k])
+        if not flip:
+            assert e_gpu[k] <= 4 * e_orc[k] + 2e-5, (k, e_gpu[k], e_orc[k])
     assert_close(p1, P, TOL_TRAIN, "post-Adam weights")
     got, want = np.array(model.last_stats().as_tuple()), np.array(st.as_tuple())
     assert_close(got[[0, 1, 2, 3, 5]], want[[0, 1, 2, 3, 5]], TOL_TRAIN, "LossStats")
