@@ -162,6 +162,42 @@ def pmc_traffic():
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+def profile_pass(which):
+    """Short runs of each kernel for rocprofv3 (--kernel-trace / --pmc): the
+    262144-env collect and random rollout, 64 train minibatches, and one 1 GiB
+    device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters."""
+    import metalgym_amd as mg
+
+    n, T = 262144, 32
+    if which in ("collect", "all"):
+        gym = mg.Gym("rollout_cartpole", n, 0)
+        model = mg.PPOModel(gym, horizon=T)
+        for _ in range(3):
+            model.collect()
+        print("profile: 3 collects of 262144 x 32", flush=True)
+        if which == "all":
+            for b in range(64):
+                mg.lib().mg_ppo_train_block(model.h, b)
+            sync()
+            print("profile: 64 train minibatches of 4096 rows", flush=True)
+        del model, gym
+    if which in ("random", "all"):
+        gym = mg.Gym("rollout_cartpole", n, 0)
+        bufs = gym.rollout_random(T)
+        for _ in range(5):
+            gym.rollout_random(T, bufs, sync=False)
+        sync()
+        print("profile: 6 random rollouts of 262144 x 32", flush=True)
+        del gym, bufs
+    if which in ("copy", "all"):
+        nbytes = 1 << 30
+        a, b = mg.DeviceBuffer(nbytes), mg.DeviceBuffer(nbytes)
+        a.zero()
+        mg.lib().mg_memcpy_d2d(b.ptr, a.ptr, nbytes)
+        sync()
+        print(f"profile: one device copy of {nbytes} bytes", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,12 +205,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--profile", choices=["collect", "random", "copy", "all"], default=None,
+                    help="run short kernel passes for rocprofv3 instead of the benchmark")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X; this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
 
     import metalgym_amd as mg
+
+    if args.profile:
+        profile_pass(args.profile)
+        return
 
     n, T = 262144, 32
     O, A = 4, 2
