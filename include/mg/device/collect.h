@@ -127,12 +127,15 @@ int launch_collect(const mg_collect_args* a) {
         a->policy.layers > MG_MAX_LAYERS)
         return MG_ERR_INVALID;
     hipStream_t st = static_cast<hipStream_t>(a->stream);
-    // 64-row tiles need n / 64 >= 2 workgroups per CU to fill the chip; smaller
-    // runs use 32-row tiles for twice the workgroups.
+    // 64-row tiles reuse each weight fragment across the most rows; they need
+    // n / 64 >= 512 workgroups (2 per CU) to fill the chip. Smaller runs use
+    // 32-row, then 16-row tiles for more workgroups.
     if (a->n >= 64u * 512u) {
         hipLaunchKernelGGL((collect_kernel<Env, 64>), dim3(a->n / 64), dim3(256), 0, st, *a);
-    } else {
+    } else if (a->n >= 32u * 256u) {
         hipLaunchKernelGGL((collect_kernel<Env, 32>), dim3(a->n / 32), dim3(256), 0, st, *a);
+    } else {
+        hipLaunchKernelGGL((collect_kernel<Env, 16>), dim3(a->n / 16), dim3(256), 0, st, *a);
     }
     return (int)hipGetLastError();
 }

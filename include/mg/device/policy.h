@@ -1,22 +1,26 @@
-// Fused residual-MLP policy forward for a tile of M rows (M = 32 or 64) on one
-// 256-thread workgroup, fp32 MFMA (v_mfma_f32_32x32x2_f32).
+// Fused residual-MLP policy forward for a tile of M rows (M = 16, 32 or 64) on
+// one 256-thread workgroup, fp32 MFMA.
 //
 // Network (model/ppo.h:575-626): embed h = obs W_in + b_in; per block
 // h += relu(LN(h) Up) Down; final LN; head = LN(h) W_head (no bias).
 //
 // Mapping: wave w owns embed columns [32w, 32w + 32) of the residual stream h,
-// held in MFMA accumulator layout (f32x16 per 32-row tile). Each block runs the
-// hidden dimension in 128-wide chunks so the hidden activations never leave the
-// CU: V_c = relu(x Up[:, c]) is computed by the four waves (32 hidden columns
+// held in MFMA accumulator layout. 32- and 64-row tiles use
+// v_mfma_f32_32x32x2_f32 (one 32-column tile per wave); 16-row tiles use
+// v_mfma_f32_16x16x4_f32 (two 16-column tiles per wave), so a 4096-row
+// minibatch still spreads over 256 workgroups. Each block runs the hidden
+// dimension in 128-wide chunks so the hidden activations never leave the CU:
+// V_c = relu(x Up[:, c]) is computed by the four waves (32 hidden columns
 // each), staged in LDS, and immediately contracted with Down[c, :] into the
 // block output accumulator. LN outputs and hidden chunks are the A operands
 // (LDS, float4 reads); weights are the B operands, read straight from L2 (the
 // whole 1 MB policy stays L2-resident across the grid).
 //
-// K-order permutation: for a group of 8 k-values, lane (m, h) reads
-// x[m][8g + 4h .. 8g + 4h + 3] as one float4 and MFMA step j contracts
-// k = 8g + 4h + j, so B supplies W[8g + 4h + j][n]. Every k is covered once;
-// only the fp32 summation order differs from a sequential loop.
+// K-order permutation: with KS k-values per MFMA step, a k-group holds 4*KS
+// k-values; lane (m, q) (q = lane / MT) reads x[m][g*4KS + 4q .. + 3] as one
+// float4 and MFMA step j contracts k = g*4KS + 4q + j, so B supplies
+// W[g*4KS + 4q + j][n]. Every k is covered once; only the fp32 summation order
+// differs from a sequential loop.
 #pragma once
 #include "common.h"
 
@@ -26,53 +30,168 @@ namespace dev {
 constexpr int kLds = kEmbed + 4;  // LDS row stride in floats (pad against bank conflicts)
 constexpr int kChunk = 128;       // hidden columns per chunk
 
+// MFMA shape used by an M-row tile.
+template <int M>
+struct Shape {
+    static constexpr int MT = M >= 32 ? 32 : 16;  // MFMA M = N
+    static constexpr int KS = MT == 32 ? 2 : 4;   // k per MFMA step
+    static constexpr int KG = 4 * KS;             // k per float4 group
+    static constexpr int RT = M / MT;             // row tiles
+    static constexpr int CT = 32 / MT;            // 32-column strips per wave, in MFMA tiles
+    static constexpr int REGS = MT == 32 ? 16 : 4;
+    using Acc = typename std::conditional<MT == 32, f32x16, f32x4>::type;
+    static_assert(M == 16 || M == 32 || M == 64, "tile rows");
+
+    __device__ static __forceinline__ Acc mfma(float a, float b, Acc c) {
+        if constexpr (MT == 32)
+            return mfma32x32x2(a, b, c);
+        else
+            return mfma16x16x4(a, b, c);
+    }
+    // Row (within the MT x MT tile) of accumulator register r of `lane`.
+    __device__ static __forceinline__ int row(int r, int lane) {
+        if constexpr (MT == 32)
+            return c32_row(r, lane);
+        else
+            return c16_row(r, lane);
+    }
+    __device__ static __forceinline__ int col(int lane) { return lane % MT; }
+    __device__ static __forceinline__ int quad(int lane) { return lane / MT; }
+};
+
 template <int M>
 struct FwdSmem {
     float xs[M * kLds];  // LN output (A operand of the up GEMM)
     float vs[M * kLds];  // relu'd hidden chunk (A operand of the down GEMM)
 };
 
+// Residual stream of an M-row tile. Element (rt, ct, r) of wave w, lane l is
+// row MT rt + Shape::row(r, l), column 32 w + MT ct + l % MT.
 template <int M>
 struct FwdRegs {
-    static constexpr int RT = M / 32;
-    f32x16 h[RT];  // residual stream; tile rt, register r -> row 32 rt + c32_row(r, lane), col 32 w + lane % 32
+    using S = Shape<M>;
+    typename S::Acc h[S::RT][S::CT];
 };
+
+template <int M>
+__device__ __forceinline__ void zero(typename Shape<M>::Acc (&a)[Shape<M>::RT][Shape<M>::CT]) {
+#pragma unroll
+    for (int rt = 0; rt < Shape<M>::RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < Shape<M>::CT; ++ct) a[rt][ct] = typename Shape<M>::Acc{};
+}
+
+// Calls f(rt, ct, r, row, col) for every accumulator element this thread holds.
+template <int M, class F>
+__device__ __forceinline__ void for_each_elem(F f) {
+    using S = Shape<M>;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < S::CT; ++ct)
+#pragma unroll
+            for (int r = 0; r < S::REGS; ++r)
+                f(rt, ct, r, S::MT * rt + S::row(r, lane), 32 * w + S::MT * ct + S::col(lane));
+}
+
+// acc[rt][ct] += A[rows][0:K] @ W[0:K][cols] for this wave's 32-column strip.
+// A is in LDS (row stride kLds, A[m][k] at a_lds[m * kLds + k]); W element
+// (k, n) is w_ptr[k * w_ld + n]; `cols` of the strip start at n0.
+template <int M, int K>
+__device__ __forceinline__ void gemm_strip(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
+                                           const float* a_lds, const float* w_ptr, size_t w_ld, int n0) {
+    using S = Shape<M>;
+    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
+    const float* ap = a_lds + n * kLds + 4 * q;
+    const float* bp = w_ptr + (size_t)(4 * q) * w_ld + n0 + n;
+#pragma unroll
+    for (int g = 0; g < K / S::KG; ++g) {
+        float b[S::CT][4];
+#pragma unroll
+        for (int ct = 0; ct < S::CT; ++ct)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[ct][j] = bp[(size_t)(S::KG * g + j) * w_ld + S::MT * ct];
+        f32x4 a[S::RT];
+#pragma unroll
+        for (int rt = 0; rt < S::RT; ++rt)
+            a[rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[rt][j], b[ct][j], acc[rt][ct]);
+    }
+}
+
+// Same with a transposed weight operand: W^T element (k, n) is wt_ptr[n * wt_ld + k],
+// so each lane's four k-values are one contiguous float4.
+template <int M, int K>
+__device__ __forceinline__ void gemm_strip_t(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
+                                             const float* a_lds, const float* wt_ptr, size_t wt_ld, int n0) {
+    using S = Shape<M>;
+    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
+    const float* ap = a_lds + n * kLds + 4 * q;
+    const float* bp = wt_ptr + (size_t)(n0 + n) * wt_ld + 4 * q;
+#pragma unroll
+    for (int g = 0; g < K / S::KG; ++g) {
+        f32x4 b[S::CT];
+#pragma unroll
+        for (int ct = 0; ct < S::CT; ++ct)
+            b[ct] = *reinterpret_cast<const f32x4*>(bp + (size_t)(S::MT * ct) * wt_ld + S::KG * g);
+        f32x4 a[S::RT];
+#pragma unroll
+        for (int rt = 0; rt < S::RT; ++rt)
+            a[rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[rt][j], b[ct][j], acc[rt][ct]);
+    }
+}
+
+// Writes a register tile to LDS (row stride kLds) and optionally to global
+// memory (row stride ld), optionally through relu.
+template <int M, bool RELU = false>
+__device__ __forceinline__ void store_tile(const typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
+                                           float* lds, float* global = nullptr, size_t ld = 0, int gcol0 = 0) {
+    for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+        float x = acc[rt][ct][r];
+        if (RELU) x = x > 0.0f ? x : 0.0f;
+        lds[row * kLds + col] = x;
+        if (global) global[(size_t)row * ld + gcol0 + col] = x;
+    });
+}
 
 // model/input.metal:11-27: h = b_in + sum_k obs[k] W_in[k], in k order.
 // obsL is [M][O] in LDS.
 template <int M>
 __device__ __forceinline__ void fwd_embed(const mg_policy_view& pv, const float* obsL, int O, FwdRegs<M>& R) {
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int col = 32 * w + (lane & 31);
-    const float* W = pv.params + pv.off_in_w + col;
-    const float b = pv.params[pv.off_in_b + col];
-#pragma unroll
-    for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) R.h[rt][r] = b;
+    const float* W = pv.params + pv.off_in_w;
+    const float* bias = pv.params + pv.off_in_b;
+    for_each_elem<M>([&](int rt, int ct, int r, int row, int col) { R.h[rt][ct][r] = bias[col]; });
     for (int k = 0; k < O; ++k) {
-        const float wk = W[k * kEmbed];
-#pragma unroll
-        for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) R.h[rt][r] += obsL[(32 * rt + c32_row(r, lane)) * O + k] * wk;
+        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+            R.h[rt][ct][r] += obsL[row * O + k] * W[k * kEmbed + col];
+        });
     }
 }
 
 // model/layernorm.metal:10-71 on the register tile; the result goes to sm.xs.
-// If xn_out/sd_out are given, the normalised values and the standard deviation
-// are also written there ([M][128] and [M], row-major) for the backward pass.
+// If xn_out/sd_out/x_out are given, the normalised values, the standard
+// deviation and the output are also written there ([M][128], [M], [M][128],
+// row-major) for the backward pass.
 template <int M>
 __device__ __forceinline__ void fwd_layernorm(FwdSmem<M>& sm, const FwdRegs<M>& R, const float* gamma,
                                               const float* beta, float* xn_out = nullptr, float* sd_out = nullptr,
                                               float* x_out = nullptr) {
     constexpr int TPR = 256 / M;       // threads per row
     constexpr int CPT = kEmbed / TPR;  // columns per thread
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-#pragma unroll
-    for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sm.xs[(32 * rt + c32_row(r, lane)) * kLds + 32 * w + (lane & 31)] = R.h[rt][r];
+    const int tid = threadIdx.x;
+    store_tile<M>(R.h, sm.xs);
     __syncthreads();
     const int row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     float* xr = sm.xs + row * kLds + c0;
@@ -120,62 +239,26 @@ __device__ __forceinline__ void fwd_layernorm(FwdSmem<M>& sm, const FwdRegs<M>& 
 template <int M>
 __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M>& R,
                                           float* v_out = nullptr) {
-    constexpr int RT = FwdRegs<M>::RT;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, hh = lane >> 5;
+    using S = Shape<M>;
+    const int w = threadIdx.x >> 6;
     const int H = (int)pv.hidden;
     const float* Up = pv.params + pv.off_up[l];
     const float* Dn = pv.params + pv.off_down[l];
-    f32x16 o[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) o[rt] = f32x16{};
+    typename S::Acc o[S::RT][S::CT];
+    zero<M>(o);
     for (int c = 0; c < H / kChunk; ++c) {
-        f32x16 v[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) v[rt] = f32x16{};
-        const float* bp = Up + (size_t)(4 * hh) * H + kChunk * c + 32 * w + n;
-        const float* ap = sm.xs + n * kLds + 4 * hh;
-#pragma unroll
-        for (int g = 0; g < kEmbed / 8; ++g) {
-            float b[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = bp[(size_t)(8 * g + j) * H];
-            f32x4 a[RT];
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) a[rt] = *reinterpret_cast<const f32x4*>(ap + 32 * rt * kLds + 8 * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) v[rt] = mfma32x32x2(a[rt][j], b[j], v[rt]);
-        }
+        typename S::Acc v[S::RT][S::CT];
+        zero<M>(v);
+        gemm_strip<M, kEmbed>(v, sm.xs, Up, H, kChunk * c + 32 * w);
         __syncthreads();  // every wave is done reading the previous chunk from vs
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 32 * rt + c32_row(r, lane);
-                const float x = v[rt][r] > 0.0f ? v[rt][r] : 0.0f;
-                sm.vs[row * kLds + 32 * w + n] = x;
-                if (v_out) v_out[(size_t)row * H + kChunk * c + 32 * w + n] = x;
-            }
+        store_tile<M, true>(v, sm.vs, v_out, H, kChunk * c);
         __syncthreads();
-        const float* dp = Dn + (size_t)(kChunk * c + 4 * hh) * kEmbed + 32 * w + n;
-        const float* vp = sm.vs + n * kLds + 4 * hh;
-#pragma unroll
-        for (int g = 0; g < kChunk / 8; ++g) {
-            float b[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = dp[(size_t)(8 * g + j) * kEmbed];
-            f32x4 a[RT];
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) a[rt] = *reinterpret_cast<const f32x4*>(vp + 32 * rt * kLds + 8 * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) o[rt] = mfma32x32x2(a[rt][j], b[j], o[rt]);
-        }
+        gemm_strip<M, kChunk>(o, sm.vs, Dn + (size_t)kChunk * c * kEmbed, kEmbed, 32 * w);
     }
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) R.h[rt] = R.h[rt] + o[rt];
+    for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < S::CT; ++ct) R.h[rt][ct] = R.h[rt][ct] + o[rt][ct];
 }
 
 // model/linear.metal:17-37: head[row][j] = sum_k xs[row][k] W_head[k][j] for

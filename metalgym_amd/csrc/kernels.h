@@ -24,20 +24,21 @@ struct TrainWs {
     float* x;         // [(L+1)][B][128] LN outputs
     float* sd;        // [(L+1)][B] LN standard deviations
     float* v;         // [L][B][H] relu'd hidden activations
-    float* dxl;       // [(L+1)][B][128] gradients at the LN outputs
     float* dhb;       // [L][B][128] gradients at the block outputs
     float* dvb;       // [L][B][H] masked hidden gradients
-    float* dh0;       // [B][128] gradient at the embed output
-    float* dhead;     // [B][HD]
-    float* rowstats;  // [B][5]
-    float* dls;       // [B][A] per-row log_std gradients (Gaussian head)
-    float* partial;   // [kSplits][count] per-split weight-gradient partial sums
+    // Per row-tile partial sums of the vector parameters, the head and the
+    // loss statistics: [B / kTileRows][tp_count], the vector group at its
+    // arena offsets (0 .. float_group), the head [128 x HD] at float_group,
+    // then the 5 LossStats sums.
+    float* tp;
+    float* partial;   // [kSplits][count] per-split sums of the block matrices' gradients
     float* grad;      // [count] the reduced gradient (pre-clip)
-    float* normpart;  // [reduce blocks]
-    float* normsq;    // [1]
-    unsigned* counter;  // [1] last-block ticket
+    float* normpart;  // [kReduceBlocks] per-workgroup squared norms
+    uint32_t tp_count;
 };
-constexpr int kSplits = 16;  // row splits of the weight-gradient reductions
+constexpr int kSplits = 16;        // row splits of the block-matrix gradient sums
+constexpr int kTileRows = 16;      // rows per train_rows workgroup
+constexpr int kReduceBlocks = 256; // workgroups of the gradient reduction
 
 struct TrainStep {
     uint32_t row0;       // first slot row of the minibatch (t * n + r0)

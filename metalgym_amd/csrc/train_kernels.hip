@@ -1,16 +1,20 @@
 // One PPO minibatch update (model/ppo.h:906-916) as four launches:
 //
-//  1. train_rows: per 32-row tile, the forward recompute with activation
-//     capture (model/ppo.h:909), the loss and head gradient
-//     (model/policy.metal:14-69 / model/gaussian.metal:76-135) and the whole
-//     backward dX chain (model/ppo.h:793-865) on fp32 MFMA, writing the
+//  1. train_rows: per 16-row tile (256 workgroups for 4096 rows), the forward
+//     recompute with activation capture (model/ppo.h:909), the loss and head
+//     gradient (model/policy.metal:14-69 / model/gaussian.metal:76-135) and the
+//     whole backward dX chain (model/ppo.h:793-865) on fp32 MFMA, writing the
 //     activations and gradients the weight gradients need.
-//  2. train_dw: every weight gradient as a sum over rows, split into kSplits
-//     row ranges: 64x64 MFMA tiles of X^T dY for the block matrices, column
-//     sums for the vector parameters, the head and log_std.
-//  3. grad_reduce: sums the splits in fixed order, the global squared norm
-//     (last-workgroup pattern, fixed order) and the minibatch's LossStats.
-//  4. adam: clip scale and Adam (model/optimizer.metal:36-60).
+//     The same workgroup writes its tile's sums of the vector-parameter, head
+//     and log_std gradients and of the loss statistics.
+//  2. train_dw: the block matrices' gradients X^T dY as LDS-staged 64x64
+//     MFMA tiles, the rows split into ranges.
+//  3. grad_reduce: sums the tile partials and the row splits in fixed order,
+//     writes the minibatch's LossStats (model/ppo.h:925-943) and one partial
+//     squared norm per workgroup.
+//  4. adam: every workgroup adds the partial norms in the same fixed order
+//     (so no cross-workgroup synchronisation is needed), applies the clip
+//     scale and Adam (model/optimizer.metal:23-60).
 //
 // Every reduction has a fixed order, so a rerun gives the same bits (the
 // reference uses float atomics for several of these).
@@ -23,9 +27,30 @@
 namespace mg {
 namespace dev {
 
-constexpr int kTR = 32;  // rows per train_rows workgroup
+constexpr int kTR = kTileRows;  // rows per train_rows workgroup
 constexpr int kMaxHeadT = 64;
 constexpr int kMaxObsT = 64;
+
+// Column sums over the tile's M rows: out[c * ostride] = sum_r a[r * lda + c] * b(r, c)
+// for the 128 embed columns, where b(r, c) is b[r * ldb + c] (ldb > 0), the
+// per-row scalar b[r * bstride] (ldb == 0), or 1 (b == nullptr). The two
+// halves of the workgroup sum half the rows each and are added in a fixed
+// order. `scratch` is 256 floats of LDS; ends with a barrier.
+template <int M>
+__device__ __forceinline__ void tile_colsum(const float* a, int lda, const float* b, int ldb, int bstride,
+                                            float* out, int ostride, float* scratch) {
+    const int t = threadIdx.x, c = t & 127, half = t >> 7;
+    float s = 0.0f;
+#pragma unroll
+    for (int r = half * (M / 2); r < (half + 1) * (M / 2); ++r) {
+        const float x = a[r * lda + c];
+        s += b ? x * (ldb ? b[r * ldb + c] : b[r * bstride]) : x;
+    }
+    scratch[t] = s;
+    __syncthreads();
+    if (t < 128) out[c * ostride] = scratch[c] + scratch[128 + c];
+    __syncthreads();
+}
 
 struct RowsArgs {
     mg_policy_view pv;
@@ -44,38 +69,28 @@ struct RowsArgs {
 // Gradient at the final LN output: dX = dZ W_head^T (model/linear.metal:40-60).
 template <int M>
 __device__ __forceinline__ void bwd_head(const mg_policy_view& pv, const float* dheadL, int HD, FwdRegs<M>& G) {
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = 32 * w + (lane & 31);
-    const float* Wh = pv.params + pv.off_head + col * HD;
-#pragma unroll
-    for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) G.h[rt][r] = 0.0f;
+    const float* Wh = pv.params + pv.off_head;
+    for_each_elem<M>([&](int rt, int ct, int r, int row, int col) { G.h[rt][ct][r] = 0.0f; });
     for (int j = 0; j < HD; ++j) {
-        const float wj = Wh[j];
-#pragma unroll
-        for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) G.h[rt][r] += dheadL[(32 * rt + c32_row(r, lane)) * HD + j] * wj;
+        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+            G.h[rt][ct][r] += dheadL[row * HD + j] * Wh[col * HD + j];
+        });
     }
 }
 
 // model/layernorm.metal:74-127 on a register tile: G holds the gradient at the
-// LN output on entry (also stored to dx_store, [M][128]) and the gradient at
-// the LN input on exit. xn/sd are the tile's forward captures.
+// LN output on entry and the gradient at the LN input on exit. xn/sd are the
+// tile's forward captures. The tile's sums for dgamma (xn * dZ) and dbeta (dZ)
+// go to tp_gamma / tp_beta (the reference adds them with float atomics).
 template <int M>
 __device__ __forceinline__ void bwd_layernorm(FwdSmem<M>& sm, FwdRegs<M>& G, const float* xn, const float* sd,
-                                              const float* gamma, float* dx_store) {
+                                              const float* gamma, float* tp_gamma, float* tp_beta, float* scratch) {
     constexpr int TPR = 256 / M, CPT = kEmbed / TPR;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = 32 * w + (lane & 31);
-#pragma unroll
-    for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = 32 * rt + c32_row(r, lane);
-            sm.xs[row * kLds + col] = G.h[rt][r];
-            dx_store[row * kEmbed + col] = G.h[rt][r];
-        }
+    const int tid = threadIdx.x;
+    store_tile<M>(G.h, sm.xs);
     __syncthreads();
+    tile_colsum<M>(sm.xs, kLds, xn, kEmbed, 0, tp_gamma, 1, scratch);
+    tile_colsum<M>(sm.xs, kLds, nullptr, 0, 0, tp_beta, 1, scratch);
     const int row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     float* zr = sm.xs + row * kLds + c0;
     const float* xr = xn + row * kEmbed + c0;
@@ -94,10 +109,7 @@ __device__ __forceinline__ void bwd_layernorm(FwdSmem<M>& sm, FwdRegs<M>& G, con
 #pragma unroll
     for (int c = 0; c < CPT; ++c) zr[c] = rd * (dxn[c] - r1 - xv[c] * r2);
     __syncthreads();
-#pragma unroll
-    for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) G.h[rt][r] = sm.xs[(32 * rt + c32_row(r, lane)) * kLds + col];
+    for_each_elem<M>([&](int rt, int ct, int r, int row2, int col) { G.h[rt][ct][r] = sm.xs[row2 * kLds + col]; });
     __syncthreads();
 }
 
@@ -109,71 +121,37 @@ __device__ __forceinline__ void bwd_layernorm(FwdSmem<M>& sm, FwdRegs<M>& G, con
 template <int M>
 __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M>& D,
                                           const float* v_tile, float* dv_store, float* dh_store, const float* xn_tile,
-                                          const float* sd_tile, float* dx_store) {
-    constexpr int RT = FwdRegs<M>::RT;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, hh = lane >> 5;
+                                          const float* sd_tile, float* tp, float* scratch) {
+    using S = Shape<M>;
+    const int w = threadIdx.x >> 6;
     const int H = (int)pv.hidden;
     const float* Up = pv.params + pv.off_up[l];
     const float* Dn = pv.params + pv.off_down[l];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = 32 * rt + c32_row(r, lane);
-            sm.xs[row * kLds + 32 * w + n] = D.h[rt][r];
-            dh_store[row * kEmbed + 32 * w + n] = D.h[rt][r];
-        }
+    store_tile<M>(D.h, sm.xs, dh_store, kEmbed, 0);
     __syncthreads();
     FwdRegs<M> G;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) G.h[rt] = f32x16{};
+    zero<M>(G.h);
     for (int c = 0; c < H / kChunk; ++c) {
-        f32x16 v[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) v[rt] = f32x16{};
-        const float* bp = Dn + (size_t)(kChunk * c + 32 * w + n) * kEmbed + 4 * hh;
-        const float* ap = sm.xs + n * kLds + 4 * hh;
-#pragma unroll
-        for (int g = 0; g < kEmbed / 8; ++g) {
-            const f32x4 b = *reinterpret_cast<const f32x4*>(bp + 8 * g);
-            f32x4 a[RT];
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) a[rt] = *reinterpret_cast<const f32x4*>(ap + 32 * rt * kLds + 8 * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) v[rt] = mfma32x32x2(a[rt][j], b[j], v[rt]);
-        }
+        typename S::Acc v[S::RT][S::CT];
+        zero<M>(v);
+        gemm_strip_t<M, kEmbed>(v, sm.xs, Dn + (size_t)kChunk * c * kEmbed, kEmbed, 32 * w);
         __syncthreads();
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 32 * rt + c32_row(r, lane);
-                const int hid = kChunk * c + 32 * w + n;
-                const float x = v_tile[(size_t)row * H + hid] > 0.0f ? v[rt][r] : 0.0f;
-                sm.vs[row * kLds + 32 * w + n] = x;
-                dv_store[(size_t)row * H + hid] = x;
-            }
+        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+            const int hid = kChunk * c + col;
+            const float x = v_tile[(size_t)row * H + hid] > 0.0f ? v[rt][ct][r] : 0.0f;
+            sm.vs[row * kLds + col] = x;
+            dv_store[(size_t)row * H + hid] = x;
+        });
         __syncthreads();
-        const float* bp2 = Up + (size_t)(32 * w + n) * H + kChunk * c + 4 * hh;
-        const float* ap2 = sm.vs + n * kLds + 4 * hh;
-#pragma unroll
-        for (int g = 0; g < kChunk / 8; ++g) {
-            const f32x4 b = *reinterpret_cast<const f32x4*>(bp2 + 8 * g);
-            f32x4 a[RT];
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) a[rt] = *reinterpret_cast<const f32x4*>(ap2 + 32 * rt * kLds + 8 * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) G.h[rt] = mfma32x32x2(a[rt][j], b[j], G.h[rt]);
-        }
+        gemm_strip_t<M, kChunk>(G.h, sm.vs, Up + kChunk * c, H, 32 * w);
     }
     __syncthreads();
-    bwd_layernorm<M>(sm, G, xn_tile, sd_tile, pv.params + pv.off_ln_gamma[l], dx_store);
+    bwd_layernorm<M>(sm, G, xn_tile, sd_tile, pv.params + pv.off_ln_gamma[l], tp + pv.off_ln_gamma[l],
+                     tp + pv.off_ln_beta[l], scratch);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) D.h[rt] = G.h[rt] + D.h[rt];  // residualAdd(dBranch, dStream)
+    for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < S::CT; ++ct) D.h[rt][ct] = G.h[rt][ct] + D.h[rt][ct];  // residualAdd(dBranch, dStream)
 }
 
 template <int M>
@@ -182,6 +160,9 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
     __shared__ float obsL[M * kMaxObsT];
     __shared__ float headL[M * kMaxHeadT];
     __shared__ float dheadL[M * kMaxHeadT];
+    __shared__ float dlsL[M * kMaxHeadT];
+    __shared__ float statL[M * 5];
+    __shared__ float scratch[256];
     FwdRegs<M> R;
     const mg_policy_view& pv = a.pv;
     const TrainWs& ws = a.ws;
@@ -191,6 +172,7 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
     const uint32_t r0 = blockIdx.x * M;           // row within the minibatch
     const size_t g0 = (size_t)a.step.row0 + r0;   // row within the slot arrays
     const int tid = threadIdx.x;
+    float* tp = ws.tp + (size_t)blockIdx.x * ws.tp_count;  // this tile's vector-parameter partials
 
     for (int idx = tid; idx < M * O; idx += 256) obsL[idx] = a.obs_slots[g0 * O + idx];
     __syncthreads();
@@ -265,58 +247,57 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
                 const float invStd = mg::expf(-ls);
                 const float d = (act[k] - h[k]) * invStd;
                 dz[k] = gLogp * d * invStd * scale;
-                ws.dls[(r0 + tid) * A + k] = (gLogp * (d * d - 1.0f) - ec) * scale;
+                dlsL[tid * A + k] = (gLogp * (d * d - 1.0f) - ec) * scale;
             }
         }
         const float vErr = h[A] - a.ret_slots[gr];
         dz[A] = a.hp.value_coef * vErr * scale;
-        float* st = ws.rowstats + (size_t)(r0 + tid) * 5;
+        float* st = statL + tid * 5;
         st[0] = policyLoss;
         st[1] = 0.5f * a.hp.value_coef * vErr * vErr;
         st[2] = entropy;
         st[3] = oldLp - logpA;
         st[4] = (fabsf(ratio - 1.0f) > clip) ? 1.0f : 0.0f;
-        for (int j = 0; j < HD; ++j) {
-            ws.dhead[(size_t)(r0 + tid) * HD + j] = dz[j];
-            if (a.head_out) a.head_out[(size_t)(r0 + tid) * HD + j] = h[j];
-        }
+        if (a.head_out)
+            for (int j = 0; j < HD; ++j) a.head_out[(size_t)(r0 + tid) * HD + j] = h[j];
     }
     __syncthreads();
+
+    // model/linear.metal:71-93 on this tile: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
+    // (sm.xs still holds the final LN output x_f)
+    for (int j = 0; j < HD; ++j)
+        tile_colsum<M>(sm.xs, kLds, dheadL + j, 0, HD, tp + pv.float_group + j, HD, scratch);
+    if (pv.continuous && tid < A) {  // model/gaussian.metal:166-168, summed over the tile in row order
+        float s = 0.0f;
+        for (int r = 0; r < M; ++r) s += dlsL[r * A + tid];
+        tp[pv.off_log_std + tid] = s;
+    }
+    if (tid >= 64 && tid < 64 + 5) {  // the tile's LossStats sums, in row order
+        const int q = tid - 64;
+        float s = 0.0f;
+        for (int r = 0; r < M; ++r) s += statL[r * 5 + q];
+        tp[pv.float_group + kEmbed * HD + q] = s;
+    }
 
     // ---- backward ----
     FwdRegs<M> D;
     bwd_head<M>(pv, dheadL, HD, D);
     bwd_layernorm<M>(sm, D, ws.xn + ((size_t)NL * B + r0) * kEmbed, ws.sd + (size_t)NL * B + r0,
-                     pv.params + pv.off_ln_gamma[NL], ws.dxl + ((size_t)NL * B + r0) * kEmbed);
+                     pv.params + pv.off_ln_gamma[NL], tp + pv.off_ln_gamma[NL], tp + pv.off_ln_beta[NL], scratch);
     for (int l = NL - 1; l >= 0; --l) {
         bwd_block<M>(pv, l, sm, D, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
                      ws.dhb + ((size_t)l * B + r0) * kEmbed, ws.xn + ((size_t)l * B + r0) * kEmbed,
-                     ws.sd + (size_t)l * B + r0, ws.dxl + ((size_t)l * B + r0) * kEmbed);
+                     ws.sd + (size_t)l * B + r0, tp, scratch);
     }
-    {
-        const int w = tid >> 6, lane = tid & 63, col = 32 * w + (lane & 31);
-#pragma unroll
-        for (int rt = 0; rt < FwdRegs<M>::RT; ++rt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                ws.dh0[(size_t)(r0 + 32 * rt + c32_row(r, lane)) * kEmbed + col] = D.h[rt][r];
-    }
+    // model/input.metal:38-60 on this tile: dW_in[k][c] = sum_r obs[r][k] dh0[r][c], db_in = sum_r dh0
+    store_tile<M>(D.h, sm.xs);
+    __syncthreads();
+    tile_colsum<M>(sm.xs, kLds, nullptr, 0, 0, tp + pv.off_in_b, 1, scratch);
+    for (int k = 0; k < O; ++k)
+        tile_colsum<M>(sm.xs, kLds, obsL + k, 0, O, tp + pv.off_in_w + k * kEmbed, 1, scratch);
 }
 
 // ---- weight gradients ---------------------------------------------------------
-
-// A column-sum segment: out[o] = sum over rows of a[r * lda + ia(o)] * b[r * ldb + ib(o)]
-// (b == nullptr: sum of the a term alone), for o < count, written at param offset `off`.
-struct Seg {
-    const float* a;
-    const float* b;
-    uint32_t lda, ldb;
-    uint32_t count;
-    uint32_t off;
-    uint32_t ncol;  // o = k * ncol + j: a index k (outer), b index j (inner); ncol = 0: both index o
-    uint32_t pad;
-};
-constexpr int kMaxSegs = 24;
 
 // A big tile job: C[m][n] = sum_r X[r][m] Y[r][n] for a 128 x H (or H x 128) matrix.
 struct BigMat {
@@ -331,141 +312,155 @@ constexpr int kMaxBig = 2 * MG_MAX_LAYERS;
 
 struct DwArgs {
     BigMat big[kMaxBig];
-    Seg seg[kMaxSegs];
-    uint32_t nbig, nseg;
+    uint32_t nbig;
     uint32_t tiles_per_big[kMaxBig];
-    uint32_t big_tiles;   // total 64x64 tiles over all big matrices
-    uint32_t small_count; // total small outputs
-    uint32_t rows;        // B
-    uint32_t splits;      // row splits (gridDim.y)
-    uint32_t count;       // arena length
+    uint32_t big_tiles;    // total 64x64 tiles over all big matrices
+    uint32_t rows;         // B
+    uint32_t splits;       // row splits (gridDim.y)
+    uint32_t count;        // arena length
     float* partial;
 };
 
+constexpr int kDwRows = 32;    // rows staged in LDS per step
+constexpr int kDwLd = 64 + 4;  // LDS row stride of a staged 64-wide slab
+
 __global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
+    __shared__ float xs[2][kDwRows * kDwLd];
+    __shared__ float ys[2][kDwRows * kDwLd];
     const uint32_t split = blockIdx.y;
     const uint32_t rowsPer = a.rows / a.splits;
     const uint32_t rb = split * rowsPer;
     float* out = a.partial + (size_t)split * a.count;
+    const int tid = threadIdx.x;
     if (blockIdx.x < a.big_tiles) {
-        // locate the matrix and tile
         uint32_t t = blockIdx.x, m = 0;
         while (t >= a.tiles_per_big[m]) t -= a.tiles_per_big[m], ++m;
         const BigMat& bm = a.big[m];
         const uint32_t ntn = bm.ndim / 64;
         const uint32_t tm = t / ntn, tn = t % ntn;
-        const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, nn = lane & 31, hh = lane >> 5;
-        const uint32_t m0 = tm * 64 + 32 * (w >> 1), n0 = tn * 64 + 32 * (w & 1);
-        const float* xp = bm.x + (size_t)(rb + 4 * hh) * bm.ldx + m0 + nn;
-        const float* yp = bm.y + (size_t)(rb + 4 * hh) * bm.ldy + n0 + nn;
-        f32x16 acc = f32x16{};
-        for (uint32_t g = 0; g < rowsPer / 8; ++g) {
-            float av[4], bv[4];
+        const int w = tid >> 6, lane = tid & 63, nn = lane & 31, hh = lane >> 5;
+        const int wm = 32 * (w >> 1), wn = 32 * (w & 1);  // this wave's 32x32 sub-tile
+        // staging: each thread moves two float4 of X and two of Y per 32-row slab
+        const int srow = tid >> 4, scol = (tid & 15) * 4;  // rows 0..15 (+16), columns 0..60
+        const float* xg = bm.x + (size_t)rb * bm.ldx + tm * 64 + scol;
+        const float* yg = bm.y + (size_t)rb * bm.ldy + tn * 64 + scol;
+        auto load = [&](int buf, uint32_t r0) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                av[j] = xp[(size_t)(8 * g + j) * bm.ldx];
-                bv[j] = yp[(size_t)(8 * g + j) * bm.ldy];
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int rr = srow + 16 * h2;
+                *reinterpret_cast<float4*>(&xs[buf][rr * kDwLd + scol]) =
+                    *reinterpret_cast<const float4*>(xg + (size_t)(r0 + rr) * bm.ldx);
+                *reinterpret_cast<float4*>(&ys[buf][rr * kDwLd + scol]) =
+                    *reinterpret_cast<const float4*>(yg + (size_t)(r0 + rr) * bm.ldy);
             }
+        };
+        f32x16 acc = f32x16{};
+        const uint32_t steps = rowsPer / kDwRows;
+        load(0, 0);
+        __syncthreads();
+        for (uint32_t s = 0; s < steps; ++s) {
+            const int cur = s & 1;
+            if (s + 1 < steps) load(cur ^ 1, (s + 1) * kDwRows);
+            const float* xc = xs[cur];
+            const float* yc = ys[cur];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = mfma32x32x2(av[j], bv[j], acc);
+            for (int g = 0; g < kDwRows / 8; ++g) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k = 8 * g + 4 * hh + j;
+                    acc = mfma32x32x2(xc[k * kDwLd + wm + nn], yc[k * kDwLd + wn + nn], acc);
+                }
+            }
+            __syncthreads();
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t row = m0 + c32_row(r, lane);
-            out[bm.off + (size_t)row * bm.ndim + n0 + nn] = acc[r];
+            const uint32_t row = tm * 64 + wm + c32_row(r, lane);
+            out[bm.off + (size_t)row * bm.ndim + tn * 64 + wn + nn] = acc[r];
         }
         return;
     }
-    const uint32_t o = (blockIdx.x - a.big_tiles) * 256 + threadIdx.x;
-    if (o >= a.small_count) return;
-    uint32_t s = 0, oo = o;
-    while (oo >= a.seg[s].count) oo -= a.seg[s].count, ++s;
-    const Seg& sg = a.seg[s];
-    const uint32_t ia = sg.ncol ? oo / sg.ncol : oo;
-    const uint32_t ib = sg.ncol ? oo % sg.ncol : oo;
-    float acc = 0.0f;
-    if (sg.b) {
-        for (uint32_t r = rb; r < rb + rowsPer; ++r) acc += sg.a[(size_t)r * sg.lda + ia] * sg.b[(size_t)r * sg.ldb + ib];
+}
+
+// The full gradient from its two sources, summed in fixed order, plus one
+// partial squared norm per workgroup:
+//  - workgroups [0, small_wgs): 64 tile-partial columns each (vector
+//    parameters, the head, then the 5 LossStats sums), four row groups of
+//    tiles per column added in order;
+//  - the rest: the block matrices, the sum of the row splits (grid-stride).
+struct ReduceArgs {
+    const float* partial;
+    const float* tp;
+    float* grad;
+    float* normpart;
+    float* mb_stats;
+    uint32_t splits, tiles, tp_count, count;
+    uint32_t float_group, off_head, head_count, small_wgs;
+    float inv_rows;
+};
+
+__global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
+    __shared__ float part[4][64];
+    __shared__ float red[4];
+    const int t = threadIdx.x;
+    float sq = 0.0f;
+    if (blockIdx.x < a.small_wgs) {
+        const uint32_t grp = t >> 6, per = a.tiles / 4;
+        const uint32_t stat0 = a.float_group + a.head_count;
+        for (uint32_t c0 = blockIdx.x * 64; c0 < stat0 + 5; c0 += a.small_wgs * 64) {
+            const uint32_t col = c0 + (t & 63);
+            float s = 0.0f;
+            if (col < stat0 + 5)
+                for (uint32_t k = grp * per; k < (grp + 1) * per; ++k) s += a.tp[(size_t)k * a.tp_count + col];
+            part[grp][t & 63] = s;
+            __syncthreads();
+            if (t < 64 && col < stat0 + 5) {
+                const float g = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+                if (col < a.float_group) {
+                    a.grad[col] = g;
+                    sq += g * g;
+                } else if (col < stat0) {
+                    a.grad[a.off_head + (col - a.float_group)] = g;
+                    sq += g * g;
+                } else {
+                    a.mb_stats[col - stat0] = g * a.inv_rows;  // model/ppo.h:925-943 means
+                }
+            }
+            __syncthreads();
+        }
     } else {
-        for (uint32_t r = rb; r < rb + rowsPer; ++r) acc += sg.a[(size_t)r * sg.lda + ia];
+        const uint32_t nw = gridDim.x - a.small_wgs;
+        for (uint32_t i = a.float_group + (blockIdx.x - a.small_wgs) * 256 + t; i < a.off_head; i += nw * 256) {
+            float g = 0.0f;
+            for (uint32_t s = 0; s < a.splits; ++s) g += a.partial[(size_t)s * a.count + i];
+            a.grad[i] = g;
+            sq += g * g;
+        }
     }
-    out[sg.off + oo] = acc;
+    sq = group_sum<64>(sq);
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = sq;
+    __syncthreads();
+    if (t == 0) a.normpart[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
 }
 
-// Sum of the splits per parameter, then the squared norm; the last workgroup
-// to finish adds the per-workgroup norms in order and the row stats.
-__global__ void __launch_bounds__(256) grad_reduce_kernel(const float* __restrict__ partial, uint32_t splits,
-                                                          uint32_t count,
-                                                          float* __restrict__ grad, float* __restrict__ normpart,
-                                                          float* __restrict__ normsq, unsigned* __restrict__ counter,
-                                                          const float* __restrict__ rowstats, uint32_t rows,
-                                                          float* __restrict__ mb_stats) {
-    __shared__ float red[256 * 5];
-    __shared__ bool last;
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    float g = 0.0f;
-    if (i < count) {
-        for (uint32_t s = 0; s < splits; ++s) g += partial[(size_t)s * count + i];
-        grad[i] = g;
-    }
-    red[threadIdx.x] = g * g;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        normpart[blockIdx.x] = red[0];
-        __threadfence();
-        last = atomicAdd(counter, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    // normsq = sum of the workgroup norms, fixed tree order
-    float s = 0.0f;
-    for (uint32_t b = threadIdx.x; b < gridDim.x; b += 256) s += normpart[b];
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    const float nsq = red[0];
-    __syncthreads();
-    // model/ppo.h:925-943: LossStats means over the minibatch rows
-    float st[5] = {0, 0, 0, 0, 0};
-    for (uint32_t r = threadIdx.x; r < rows; r += 256)
-#pragma unroll
-        for (int q = 0; q < 5; ++q) st[q] += rowstats[(size_t)r * 5 + q];
-#pragma unroll
-    for (int q = 0; q < 5; ++q) red[q * 256 + threadIdx.x] = st[q];
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o)
-#pragma unroll
-            for (int q = 0; q < 5; ++q) red[q * 256 + threadIdx.x] += red[q * 256 + threadIdx.x + o];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        normsq[0] = nsq;
-        const float inv = 1.0f / (float)rows;
-#pragma unroll
-        for (int q = 0; q < 5; ++q) mb_stats[q] = red[q * 256] * inv;
-        mb_stats[5] = sqrtf(nsq);
-        *counter = 0u;
-    }
-}
-
-// model/optimizer.metal:36-60
+// model/optimizer.metal:36-60; workgroup 0 also records the pre-clip norm.
 __global__ void __launch_bounds__(256) adam_kernel(float* __restrict__ param, const float* __restrict__ grad,
                                                    float* __restrict__ mom, float* __restrict__ var,
-                                                   const float* __restrict__ normsq, uint32_t count, float lr,
-                                                   float beta1_pow, float beta2_pow, float max_grad_norm) {
+                                                   const float* __restrict__ normpart, uint32_t count, float lr,
+                                                   float beta1_pow, float beta2_pow, float max_grad_norm,
+                                                   float* __restrict__ mb_stats) {
+    // Every wave adds the kReduceBlocks partial norms in the same order, so all
+    // workgroups see the same norm without synchronising with each other.
+    const int lane = threadIdx.x & 63;
+    float ns = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kReduceBlocks / 64; ++k) ns += normpart[lane + 64 * k];
+    const float norm = sqrtf(group_sum<64>(ns));
+    if (blockIdx.x == 0 && threadIdx.x == 0) mb_stats[5] = norm;
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= count) return;
     const float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f;
-    const float norm = sqrtf(normsq[0]);
     const float scale = (max_grad_norm > 0.0f && norm > max_grad_norm) ? max_grad_norm / (norm + 1e-6f) : 1.0f;
     const float g = grad[i] * scale;
     const float m = beta1 * mom[i] + (1.0f - beta1) * g;
@@ -483,33 +478,29 @@ namespace {
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 struct WsPlan {
-    size_t off[16];
+    size_t off[10];
     size_t total;
+    uint32_t tp_count;
 };
 
 WsPlan plan(const mg_policy_view& pv, uint32_t B) {
-    const size_t E = MG_EMBED, L = pv.layers, H = pv.hidden, HD = pv.head_dim, A = pv.act_dim;
-    const size_t sizes[16] = {
-        (L + 1) * B * E * 4,               // xn
-        (L + 1) * B * E * 4,               // x
-        (L + 1) * B * 4,                   // sd
-        L * B * H * 4,                     // v
-        (L + 1) * B * E * 4,               // dxl
-        L * B * E * 4,                     // dhb
-        L * B * H * 4,                     // dvb
-        B * E * 4,                         // dh0
-        B * HD * 4,                        // dhead
-        B * 5 * 4,                         // rowstats
-        B * (A ? A : 1) * 4,               // dls
-        (size_t)kSplits * pv.count * 4,  // partial
-        (size_t)pv.count * 4,              // grad
-        (((size_t)pv.count + 255) / 256) * 4,  // normpart
-        4,                                 // normsq
-        4,                                 // counter
-    };
+    const size_t E = MG_EMBED, L = pv.layers, H = pv.hidden, HD = pv.head_dim;
     WsPlan p;
+    p.tp_count = (uint32_t)align256(pv.float_group + E * HD + 5);
+    const size_t sizes[10] = {
+        (L + 1) * B * E * 4,                       // xn
+        (L + 1) * B * E * 4,                       // x
+        (L + 1) * B * 4,                           // sd
+        L * B * H * 4,                             // v
+        L * B * E * 4,                             // dhb
+        L * B * H * 4,                             // dvb
+        (size_t)(B / kTileRows) * p.tp_count * 4,  // tp
+        (size_t)kSplits * pv.count * 4,            // partial
+        (size_t)pv.count * 4,                      // grad
+        (size_t)kReduceBlocks * 4,                 // normpart
+    };
     size_t o = 0;
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < 10; ++k) {
         p.off[k] = o;
         o += align256(sizes[k]);
     }
@@ -530,18 +521,13 @@ int train_ws_bind(const mg_policy_view& pv, uint32_t rows, void* base, TrainWs* 
     ws->x = (float*)(b + p.off[1]);
     ws->sd = (float*)(b + p.off[2]);
     ws->v = (float*)(b + p.off[3]);
-    ws->dxl = (float*)(b + p.off[4]);
-    ws->dhb = (float*)(b + p.off[5]);
-    ws->dvb = (float*)(b + p.off[6]);
-    ws->dh0 = (float*)(b + p.off[7]);
-    ws->dhead = (float*)(b + p.off[8]);
-    ws->rowstats = (float*)(b + p.off[9]);
-    ws->dls = (float*)(b + p.off[10]);
-    ws->partial = (float*)(b + p.off[11]);
-    ws->grad = (float*)(b + p.off[12]);
-    ws->normpart = (float*)(b + p.off[13]);
-    ws->normsq = (float*)(b + p.off[14]);
-    ws->counter = (unsigned*)(b + p.off[15]);
+    ws->dhb = (float*)(b + p.off[4]);
+    ws->dvb = (float*)(b + p.off[5]);
+    ws->tp = (float*)(b + p.off[6]);
+    ws->partial = (float*)(b + p.off[7]);
+    ws->grad = (float*)(b + p.off[8]);
+    ws->normpart = (float*)(b + p.off[9]);
+    ws->tp_count = p.tp_count;
     return MG_OK;
 }
 
@@ -551,11 +537,13 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
                       const float* adv_stats, float* m, float* v, float* head_out, float* mb_stats) {
     const uint32_t B = step.rows;
     MG_CHECK(B % 64 == 0, MG_ERR_INVALID, "train: minibatch %u must be a multiple of 64", B);
-    // row splits of the weight-gradient sums: each split covers a multiple of 8 rows
-    const uint32_t splits = (B % (8 * kSplits) == 0) ? (uint32_t)kSplits : (uint32_t)kSplits / 2;
     MG_CHECK(pv.obs_dim <= (uint32_t)dev::kMaxObsT && pv.head_dim <= (uint32_t)dev::kMaxHeadT, MG_ERR_INVALID,
              "train: OBS_DIM <= 64 and ACT_DIM + 1 <= 64 required");
-    const uint32_t E = MG_EMBED, L = pv.layers, H = pv.hidden, HD = pv.head_dim, A = pv.act_dim, O = pv.obs_dim;
+    // row splits of the block-matrix gradient sums: each split covers a multiple of 32 rows
+    uint32_t splits = kSplits;
+    while (splits > 1 && B % (splits * dev::kDwRows) != 0) splits /= 2;
+    MG_CHECK(B % (splits * dev::kDwRows) == 0, MG_ERR_INVALID, "train: minibatch %u must be a multiple of 32", B);
+    const uint32_t E = MG_EMBED, L = pv.layers, H = pv.hidden;
 
     {  // 1. rows
         TimedLaunch tl(MG_K_TRAIN_ROWS, st);
@@ -574,7 +562,7 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         hipLaunchKernelGGL((dev::train_rows_kernel<dev::kTR>), dim3(B / dev::kTR), dim3(256), 0, st, ra);
         MG_HIP(hipGetLastError(), "train rows launch");
     }
-    {  // 2. weight gradients
+    {  // 2. block-matrix weight gradients
         TimedLaunch tl(MG_K_TRAIN_DW, st);
         dev::DwArgs da;
         memset(&da, 0, sizeof(da));
@@ -595,39 +583,35 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         }
         da.nbig = nb;
         da.big_tiles = tiles;
-        uint32_t ns = 0, small = 0;
-        auto seg = [&](const float* a, const float* b, uint32_t lda, uint32_t ldb, uint32_t count, uint32_t off,
-                       uint32_t ncol) {
-            da.seg[ns++] = {a, b, lda, ldb, count, off, ncol, 0};
-            small += count;
-        };
-        // model/input.metal:38-60: dW_in[k][c] = sum_r obs[r][k] dh0[r][c]; db_in = sum_r dh0
-        seg(obs_slots + (size_t)step.row0 * O, ws.dh0, O, E, O * E, pv.off_in_w, E);
-        seg(ws.dh0, nullptr, E, 0, E, pv.off_in_b, 0);
-        for (uint32_t l = 0; l <= L; ++l) {  // model/layernorm.metal:80-81
-            seg(ws.xn + (size_t)l * B * E, ws.dxl + (size_t)l * B * E, E, E, E, pv.off_ln_gamma[l], 0);
-            seg(ws.dxl + (size_t)l * B * E, nullptr, E, 0, E, pv.off_ln_beta[l], 0);
-        }
-        // model/linear.metal:71-93: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
-        seg(ws.x + (size_t)L * B * E, ws.dhead, E, HD, E * HD, pv.off_head, HD);
-        if (pv.continuous) seg(ws.dls, nullptr, A, 0, A, pv.off_log_std, 0);
-        da.nseg = ns;
-        da.small_count = small;
-        dim3 grid(tiles + (small + 255) / 256, splits);
-        hipLaunchKernelGGL(dev::train_dw_kernel, grid, dim3(256), 0, st, da);
+        hipLaunchKernelGGL(dev::train_dw_kernel, dim3(tiles, splits), dim3(256), 0, st, da);
         MG_HIP(hipGetLastError(), "train dW launch");
     }
-    const uint32_t rblocks = (pv.count + 255) / 256;
-    {  // 3. reduce + norm + stats
+    {  // 3. gradient assembly + partial norms
         TimedLaunch tl(MG_K_GRAD_REDUCE, st);
-        hipLaunchKernelGGL(dev::grad_reduce_kernel, dim3(rblocks), dim3(256), 0, st, ws.partial, splits, pv.count, ws.grad,
-                           ws.normpart, ws.normsq, ws.counter, ws.rowstats, B, mb_stats);
+        dev::ReduceArgs ga;
+        ga.partial = ws.partial;
+        ga.tp = ws.tp;
+        ga.grad = ws.grad;
+        ga.normpart = ws.normpart;
+        ga.splits = splits;
+        ga.tiles = B / kTileRows;
+        ga.tp_count = ws.tp_count;
+        ga.count = pv.count;
+        ga.float_group = pv.float_group;
+        ga.off_head = pv.off_head;
+        ga.head_count = E * pv.head_dim;
+        ga.mb_stats = mb_stats;
+        ga.inv_rows = 1.0f / (float)B;
+        // 64 tile-partial columns per small workgroup, at most half the grid
+        const uint32_t cols = pv.float_group + E * pv.head_dim + 5;
+        ga.small_wgs = (cols + 63) / 64 < kReduceBlocks / 2 ? (cols + 63) / 64 : kReduceBlocks / 2;
+        hipLaunchKernelGGL(dev::grad_reduce_kernel, dim3(kReduceBlocks), dim3(256), 0, st, ga);
         MG_HIP(hipGetLastError(), "grad reduce launch");
     }
     {  // 4. Adam
         TimedLaunch tl(MG_K_ADAM, st);
-        hipLaunchKernelGGL(dev::adam_kernel, dim3(rblocks), dim3(256), 0, st, pv.params, ws.grad, m, v, ws.normsq,
-                           pv.count, lr, step.beta1_pow, step.beta2_pow, hp.max_grad_norm);
+        hipLaunchKernelGGL(dev::adam_kernel, dim3((pv.count + 255) / 256), dim3(256), 0, st, pv.params, ws.grad, m, v,
+                           ws.normpart, pv.count, lr, step.beta1_pow, step.beta2_pow, hp.max_grad_norm, mb_stats);
         MG_HIP(hipGetLastError(), "adam launch");
     }
     return MG_OK;
