@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MG_ABI_VERSION 1
+#define MG_ABI_VERSION 2
 #define MG_MAX_LAYERS 8
 #define MG_EMBED 128 /* the reference's N_EMBED_CFG (model/config.h:7) */
 
@@ -96,9 +96,15 @@ typedef struct mg_rollout_args {
  * ln_gamma/ln_beta [128], final ln_gamma/ln_beta [128], log_std [act]
  * (Gaussian head only); then per block up [128 x hidden] and down [hidden x 128]
  * (row-major, x @ W), then head [128 x head_dim], head_dim = act + 1
- * (columns < act: logits or means, column act: value). */
+ * (columns < act: logits or means, column act: value).
+ * params_t holds the block matrices again, transposed, at the same offsets:
+ * up^T [hidden x 128] at off_up[l], down^T [128 x hidden] at off_down[l]
+ * (other entries unused). The library derives it from params at creation, in
+ * every Adam step and in mg_ppo_set_params / mg_ppo_params_updated; the
+ * fused forward reads the matrices from it. */
 typedef struct mg_policy_view {
     float* params;
+    float* params_t;
     uint32_t obs_dim;
     uint32_t act_dim;
     uint32_t embed;
@@ -291,6 +297,12 @@ int mg_ppo_slots_get(mg_ppo* model, mg_ppo_slots* out);
  * after train). */
 int mg_ppo_head(mg_ppo* model, const float** head, uint32_t* rows, uint32_t* head_dim);
 int mg_ppo_policy(mg_ppo* model, mg_policy_view* out);
+/* Replaces all parameters (count = mg_policy_view.count floats from host
+ * memory) and re-derives params_t. No reference counterpart: the reference's
+ * weights are shared CPU/GPU memory that tests write in place. */
+int mg_ppo_set_params(mg_ppo* model, const float* host, uint32_t count);
+/* Re-derives params_t after the caller wrote params through the device view. */
+int mg_ppo_params_updated(mg_ppo* model);
 /* Adam state: first and second moments, same layout as the parameters. */
 int mg_ppo_adam_state(mg_ppo* model, float** m, float** v, uint32_t* step);
 /* model/ppo.h:460-469 (Gaussian head only). */

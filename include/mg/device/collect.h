@@ -24,8 +24,10 @@ struct CollectSmem {
     float head[M * HD];
 };
 
+// 64- and 32-row tiles run two workgroups per CU; 16-row tiles serve runs of
+// at most 512 workgroups and get the whole register file instead.
 template <typename Env, int M>
-__global__ void __launch_bounds__(256, 2) collect_kernel(const mg_collect_args a) {
+__global__ void __launch_bounds__(256, M == 16 ? 1 : 2) collect_kernel(const mg_collect_args a) {
     using Tr = EnvTraits<Env>;
     using State = typename Env::State;
     using Action = typename Env::Action;

@@ -29,6 +29,7 @@ namespace dev {
 
 constexpr int kLds = kEmbed + 4;  // LDS row stride in floats (pad against bank conflicts)
 constexpr int kChunk = 128;       // hidden columns per chunk
+static_assert(kChunk == kEmbed, "every chunk GEMM contracts over 128");
 
 // MFMA shape used by an M-row tile.
 template <int M>
@@ -95,23 +96,41 @@ __device__ __forceinline__ void for_each_elem(F f) {
                 f(rt, ct, r, S::MT * rt + S::row(r, lane), 32 * w + S::MT * ct + S::col(lane));
 }
 
-// acc[rt][ct] += A[rows][0:K] @ W[0:K][cols] for this wave's 32-column strip.
-// A is in LDS (row stride kLds, A[m][k] at a_lds[m * kLds + k]); W element
-// (k, n) is w_ptr[k * w_ld + n]; `cols` of the strip start at n0.
-template <int M, int K>
-__device__ __forceinline__ void gemm_strip(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
-                                           const float* a_lds, const float* w_ptr, size_t w_ld, int n0) {
+// B operand (weights) of NG k-groups of a 128-deep chunk GEMM for one wave's
+// 32-column strip, held in registers.
+template <int M, int NG>
+struct BFrag {
+    float b[NG][Shape<M>::CT][4];
+};
+
+// Loads k-groups [g0, g0 + NG) of a transposed weight operand: W^T element
+// (k, n) at wt_ptr[n * wt_ld + k], so each lane's four k-values are one
+// contiguous float4.
+template <int M, int NG>
+__device__ __forceinline__ void load_frag_t(BFrag<M, NG>& f, const float* wt_ptr, size_t wt_ld, int g0) {
+    using S = Shape<M>;
+    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane), n0 = 32 * (threadIdx.x >> 6);
+    const float* bp = wt_ptr + (size_t)(n0 + n) * wt_ld + 4 * q + S::KG * g0;
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int ct = 0; ct < S::CT; ++ct) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(bp + (size_t)(S::MT * ct) * wt_ld + S::KG * g);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
+        }
+}
+
+// acc[rt][ct] += A[rows][k-groups g0 .. g0 + NG) @ B for this wave's strip. A
+// is in LDS (row stride kLds, A[m][k] at a_lds[m * kLds + k]).
+template <int M, int NG>
+__device__ __forceinline__ void gemm_frag(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
+                                          const float* a_lds, const BFrag<M, NG>& f, int g0) {
     using S = Shape<M>;
     const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
-    const float* ap = a_lds + n * kLds + 4 * q;
-    const float* bp = w_ptr + (size_t)(4 * q) * w_ld + n0 + n;
+    const float* ap = a_lds + n * kLds + 4 * q + S::KG * g0;
 #pragma unroll
-    for (int g = 0; g < K / S::KG; ++g) {
-        float b[S::CT][4];
-#pragma unroll
-        for (int ct = 0; ct < S::CT; ++ct)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[ct][j] = bp[(size_t)(S::KG * g + j) * w_ld + S::MT * ct];
+    for (int g = 0; g < NG; ++g) {
         f32x4 a[S::RT];
 #pragma unroll
         for (int rt = 0; rt < S::RT; ++rt)
@@ -121,37 +140,71 @@ __device__ __forceinline__ void gemm_strip(typename Shape<M>::Acc (&acc)[Shape<M
 #pragma unroll
             for (int rt = 0; rt < S::RT; ++rt)
 #pragma unroll
-                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[rt][j], b[ct][j], acc[rt][ct]);
+                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[rt][j], f.b[g][ct][j], acc[rt][ct]);
     }
 }
 
-// Same with a transposed weight operand: W^T element (k, n) is wt_ptr[n * wt_ld + k],
-// so each lane's four k-values are one contiguous float4.
-template <int M, int K>
-__device__ __forceinline__ void gemm_strip_t(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
-                                             const float* a_lds, const float* wt_ptr, size_t wt_ld, int n0) {
-    using S = Shape<M>;
-    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
-    const float* ap = a_lds + n * kLds + 4 * q;
-    const float* bp = wt_ptr + (size_t)(n0 + n) * wt_ld + 4 * q;
-#pragma unroll
-    for (int g = 0; g < K / S::KG; ++g) {
-        f32x4 b[S::CT];
-#pragma unroll
-        for (int ct = 0; ct < S::CT; ++ct)
-            b[ct] = *reinterpret_cast<const f32x4*>(bp + (size_t)(S::MT * ct) * wt_ld + S::KG * g);
-        f32x4 a[S::RT];
-#pragma unroll
-        for (int rt = 0; rt < S::RT; ++rt)
-            a[rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int rt = 0; rt < S::RT; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[rt][j], b[ct][j], acc[rt][ct]);
+// Where the s-th weight operand of a GEMM sequence lives (transposed layout).
+struct FragSrc {
+    const float* p;
+    uint32_t ld;
+};
+
+// Register double buffer for a sequence of 128-deep chunk GEMMs whose weight
+// operands are known in advance (a forward or backward pass). The loads of a
+// later GEMM's weights are issued as soon as registers free up, so their L2
+// latency overlaps the MFMA work (and the barriers) in between instead of
+// stalling every k-group.
+//  - 16-row tiles (one workgroup per CU, registers to spare): two whole
+//    fragments, one per GEMM role, each refilled two GEMMs ahead.
+//  - 32/64-row tiles (two workgroups per CU): the two halves of the current
+//    GEMM's fragment, each refilled with the next GEMM's half once consumed.
+template <int M>
+struct WStream {
+    static constexpr int NGF = kEmbed / Shape<M>::KG;  // k-groups of one 128-deep GEMM
+    static constexpr bool WHOLE = M == 16;
+    static constexpr int NG = WHOLE ? NGF : NGF / 2;
+    BFrag<M, NG> b[2];
+    int total;  // GEMMs in the sequence
+
+    template <class Src>
+    __device__ __forceinline__ void start(int n, Src src) {
+        total = n;
+        const FragSrc f0 = src(0);
+        if constexpr (WHOLE) {
+            load_frag_t<M, NG>(b[0], f0.p, f0.ld, 0);
+            if (n > 1) {
+                const FragSrc f1 = src(1);
+                load_frag_t<M, NG>(b[1], f1.p, f1.ld, 0);
+            }
+        } else {
+            load_frag_t<M, NG>(b[0], f0.p, f0.ld, 0);
+            load_frag_t<M, NG>(b[1], f0.p, f0.ld, NG);
+        }
     }
-}
+
+    // acc += A @ W_s for the s-th GEMM of the sequence (ROLE = s & 1), then
+    // refills the consumed registers.
+    template <int ROLE, class Src>
+    __device__ __forceinline__ void gemm(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
+                                         const float* a_lds, int s, Src src) {
+        if constexpr (WHOLE) {
+            gemm_frag<M, NG>(acc, a_lds, b[ROLE], 0);
+            if (s + 2 < total) {
+                const FragSrc f = src(s + 2);
+                load_frag_t<M, NG>(b[ROLE], f.p, f.ld, 0);
+            }
+        } else {
+            const bool more = s + 1 < total;
+            FragSrc f{nullptr, 0};
+            if (more) f = src(s + 1);
+            gemm_frag<M, NG>(acc, a_lds, b[0], 0);
+            if (more) load_frag_t<M, NG>(b[0], f.p, f.ld, 0);
+            gemm_frag<M, NG>(acc, a_lds, b[1], NG);
+            if (more) load_frag_t<M, NG>(b[1], f.p, f.ld, NG);
+        }
+    }
+};
 
 // Writes a register tile to LDS (row stride kLds) and optionally to global
 // memory (row stride ld), optionally through relu.
@@ -232,33 +285,49 @@ __device__ __forceinline__ void fwd_layernorm(FwdSmem<M>& sm, const FwdRegs<M>& 
     __syncthreads();
 }
 
+// The forward's GEMM sequence: for block l and chunk c, GEMM 2 (l NC + c)
+// is V_c = xs Up[:, c] (weights Up^T rows c, [H][128]) and the next one is
+// h += V_c Down[c, :] (weights Down^T columns c, [128][H]); both from the
+// transposed copies in params_t.
+struct FwdSeq {
+    const mg_policy_view* pv;
+    int nc;
+    __device__ __forceinline__ FragSrc operator()(int s) const {
+        const int l = s / (2 * nc), c = (s >> 1) % nc;
+        if ((s & 1) == 0) return {pv->params_t + pv->off_up[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
+        return {pv->params_t + pv->off_down[l] + kChunk * c, pv->hidden};
+    }
+};
+
 // One residual block (model/mlp.metal:18-86 + model/elementwise.metal:4-13):
-// h += relu(xs Up) Down, the hidden dimension in 128-wide chunks. xs holds
-// LN(h). If v_out is given, the relu'd hidden activations are also written
-// there ([M][hidden], row-major).
+// h += relu(xs Up) Down, the hidden dimension in 128-wide chunks whose Down
+// products accumulate straight into the residual stream (the residual add
+// folded into the GEMM accumulator). xs holds LN(h); ws streams the forward
+// sequence (FwdSeq). If v_out is given, the relu'd hidden activations are
+// also written there ([M][hidden], row-major).
 template <int M>
 __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M>& R,
-                                          float* v_out = nullptr) {
+                                          WStream<M>& ws, float* v_out = nullptr) {
     using S = Shape<M>;
-    const int w = threadIdx.x >> 6;
-    const int H = (int)pv.hidden;
-    const float* Up = pv.params + pv.off_up[l];
-    const float* Dn = pv.params + pv.off_down[l];
-    typename S::Acc o[S::RT][S::CT];
-    zero<M>(o);
-    for (int c = 0; c < H / kChunk; ++c) {
+    const int H = (int)pv.hidden, NC = H / kChunk;
+    const FwdSeq seq{&pv, NC};
+    for (int c = 0; c < NC; ++c) {
+        const int s = 2 * (l * NC + c);
         typename S::Acc v[S::RT][S::CT];
         zero<M>(v);
-        gemm_strip<M, kEmbed>(v, sm.xs, Up, H, kChunk * c + 32 * w);
+        ws.template gemm<0>(v, sm.xs, s, seq);
         __syncthreads();  // every wave is done reading the previous chunk from vs
         store_tile<M, true>(v, sm.vs, v_out, H, kChunk * c);
         __syncthreads();
-        gemm_strip<M, kChunk>(o, sm.vs, Dn + (size_t)kChunk * c * kEmbed, kEmbed, 32 * w);
+        ws.template gemm<1>(R.h, sm.vs, s + 1, seq);
     }
-#pragma unroll
-    for (int rt = 0; rt < S::RT; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < S::CT; ++ct) R.h[rt][ct] = R.h[rt][ct] + o[rt][ct];
+}
+
+// Starts the forward GEMM sequence.
+template <int M>
+__device__ __forceinline__ void fwd_start(const mg_policy_view& pv, WStream<M>& ws) {
+    const int NC = (int)pv.hidden / kChunk;
+    ws.start(2 * (int)pv.layers * NC, FwdSeq{&pv, NC});
 }
 
 // model/linear.metal:17-37: head[row][j] = sum_k xs[row][k] W_head[k][j] for
@@ -286,10 +355,12 @@ __device__ __forceinline__ void fwd_head(const mg_policy_view& pv, FwdSmem<M>& s
 template <int M>
 __device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem<M>& sm, FwdRegs<M>& R,
                                                const float* obsL, int O, float* headL, int HD) {
+    WStream<M> ws;
+    fwd_start<M>(pv, ws);
     fwd_embed<M>(pv, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
         fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l]);
-        fwd_block<M>(pv, (int)l, sm, R);
+        fwd_block<M>(pv, (int)l, sm, R, ws);
     }
     fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[pv.layers], pv.params + pv.off_ln_beta[pv.layers]);
     fwd_head<M>(pv, sm, headL, HD);

@@ -31,7 +31,7 @@ class EnvDesc(C.Structure):
 
 
 class PolicyView(C.Structure):
-    _fields_ = [("params", P)] + [(n, u32) for n in ("obs_dim", "act_dim", "embed", "hidden", "layers", "head_dim",
+    _fields_ = [("params", P), ("params_t", P)] + [(n, u32) for n in ("obs_dim", "act_dim", "embed", "hidden", "layers", "head_dim",
                                                        "continuous", "count", "off_in_w", "off_in_b")] + [
         ("off_ln_gamma", u32 * (MAX_LAYERS + 1)),
         ("off_ln_beta", u32 * (MAX_LAYERS + 1)),
@@ -134,6 +134,8 @@ def lib():
         "mg_ppo_slots_get": (I, [P, P]),
         "mg_ppo_head": (I, [P, P, P, P]),
         "mg_ppo_policy": (I, [P, P]),
+        "mg_ppo_set_params": (I, [P, P, u32]),
+        "mg_ppo_params_updated": (I, [P]),
         "mg_ppo_adam_state": (I, [P, P, P, P]),
         "mg_ppo_set_log_std": (I, [P, f32]),
         "mg_ppo_last_order": (I, [P, P, u32, P]),
@@ -413,7 +415,8 @@ class PPOModel:
 
     def set_params(self, p: np.ndarray) -> None:
         assert p.shape == (self.pv.count,)
-        h2d(self.pv.params, np.ascontiguousarray(p, np.float32))
+        p = np.ascontiguousarray(p, np.float32)
+        check(lib().mg_ppo_set_params(self.h, p.ctypes.data_as(C.c_void_p), self.pv.count))
 
     def adam_state(self):
         m, v, st = C.c_void_p(), C.c_void_p(), u32()

@@ -48,6 +48,12 @@ struct TrainStep {
     float beta1_pow, beta2_pow;
 };
 
+// params_t (the transposed block matrices) from params.
+int launch_transpose_blocks(hipStream_t st, const mg_policy_view& pv);
+// MG_OK if the block matrices sit contiguously from float_group (the layout
+// the Adam and transpose kernels tile).
+int check_matrix_layout(const mg_policy_view& pv);
+
 int train_ws_bytes(const mg_policy_view& pv, uint32_t rows, size_t* bytes);
 int train_ws_bind(const mg_policy_view& pv, uint32_t rows, void* base, TrainWs* ws);
 // One minibatch: rows pass, weight-gradient pass, reduce + norm, Adam.

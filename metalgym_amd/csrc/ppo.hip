@@ -255,7 +255,9 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
     const size_t n = p->n, T = p->T;
     const size_t slot = T * n;
     int rc;
+    if ((rc = check_matrix_layout(pv))) return fail(rc);
     if ((rc = device_alloc((void**)&pv.params, (size_t)pv.count * 4, "PPOModel params")) ||
+        (rc = device_alloc((void**)&pv.params_t, (size_t)pv.count * 4, "PPOModel transposed matrices")) ||
         (rc = device_alloc((void**)&p->m, (size_t)pv.count * 4, "PPOModel adam m")) ||
         (rc = device_alloc((void**)&p->v, (size_t)pv.count * 4, "PPOModel adam v")) ||
         (rc = device_alloc((void**)&p->obs_slots, (T + 1) * n * env->obs_dim * 4, "obs slots")) ||
@@ -284,7 +286,10 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
         hipMemsetAsync(p->adv, 0, slot * 4, st) != hipSuccess ||
         hipMemsetAsync(p->ret, 0, slot * 4, st) != hipSuccess ||
         hipMemsetAsync(p->head, 0, (size_t)p->head_cap * pv.head_dim * 4, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess)
+        hipMemsetAsync(pv.params_t, 0, (size_t)pv.count * 4, st) != hipSuccess)
+        return fail(set_error(MG_ERR_HIP, "PPOModel: initialisation upload failed"));
+    if ((rc = launch_transpose_blocks(st, pv))) return fail(rc);
+    if (hipStreamSynchronize(st) != hipSuccess)
         return fail(set_error(MG_ERR_HIP, "PPOModel: initialisation upload failed"));
     p->order.resize(p->blocks);
     for (uint32_t b = 0; b < p->blocks; ++b) p->order[b] = b;
@@ -297,6 +302,7 @@ int mg_ppo_destroy(mg_ppo* p) {
     if (!p) return MG_OK;
     if (p->gym && p->gym->stream) (void)hipStreamSynchronize(p->gym->stream);
     (void)hipFree(p->pv.params);
+    (void)hipFree(p->pv.params_t);
     (void)hipFree(p->m);
     (void)hipFree(p->v);
     (void)hipFree(p->obs_slots);
@@ -460,6 +466,23 @@ int mg_ppo_head(mg_ppo* p, const float** head, uint32_t* rows, uint32_t* head_di
 int mg_ppo_policy(mg_ppo* p, mg_policy_view* out) {
     MG_CHECK(p && out, MG_ERR_INVALID, "policy: null argument");
     *out = p->pv;
+    return MG_OK;
+}
+
+int mg_ppo_set_params(mg_ppo* p, const float* host, uint32_t count) {
+    MG_CHECK(p && host, MG_ERR_INVALID, "set_params: null argument");
+    MG_CHECK(count == p->pv.count, MG_ERR_INVALID, "set_params: %u floats given, the arena holds %u", count,
+             p->pv.count);
+    MG_HIP(hipMemcpyAsync(p->pv.params, host, (size_t)count * 4, hipMemcpyHostToDevice, p->gym->stream),
+           "set_params upload");
+    return mg_ppo_params_updated(p);
+}
+
+int mg_ppo_params_updated(mg_ppo* p) {
+    MG_CHECK(p, MG_ERR_INVALID, "params_updated: null model");
+    int rc = launch_transpose_blocks(p->gym->stream, p->pv);
+    if (rc) return rc;
+    MG_HIP(hipStreamSynchronize(p->gym->stream), "params_updated synchronize");
     return MG_OK;
 }
 

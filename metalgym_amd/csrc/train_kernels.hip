@@ -113,37 +113,56 @@ __device__ __forceinline__ void bwd_layernorm(FwdSmem<M>& sm, FwdRegs<M>& G, con
     __syncthreads();
 }
 
+// The backward's GEMM sequence, blocks in reverse: for block l and chunk c,
+// GEMM 2 ((L - 1 - l) NC + c) is dV_c = dh Down[c, :]^T (weights Down rows c,
+// [128 hidden][128]) and the next one is dx += dV_c Up[:, c]^T (weights Up
+// columns c, [128][H]); both are the arena's own row-major matrices read as
+// transposed operands.
+struct BwdSeq {
+    const mg_policy_view* pv;
+    int nc;
+    __device__ __forceinline__ FragSrc operator()(int s) const {
+        const int l = (int)pv->layers - 1 - s / (2 * nc), c = (s >> 1) % nc;
+        if ((s & 1) == 0) return {pv->params + pv->off_down[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
+        return {pv->params + pv->off_up[l] + kChunk * c, pv->hidden};
+    }
+};
+
 // Backward of block l (model/mlp.metal:88-153 + model/ppo.h:851-852). D holds
 // the gradient at the block output (dStream) and is updated in place to the
 // gradient at the block input. Chunked like the forward: dV_c = (dh Down_c^T)
 // masked by relu, then dx += dV_c Up_c^T; both weight reads are contiguous
-// float4s along the contraction.
+// float4s along the contraction; ws streams the backward sequence (BwdSeq).
 template <int M>
 __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M>& D,
-                                          const float* v_tile, float* dv_store, float* dh_store, const float* xn_tile,
-                                          const float* sd_tile, float* tp, float* scratch) {
+                                          WStream<M>& ws, const float* v_tile, float* dv_store, float* dh_store,
+                                          const float* xn_tile, const float* sd_tile, float* tp, float* scratch) {
     using S = Shape<M>;
-    const int w = threadIdx.x >> 6;
-    const int H = (int)pv.hidden;
-    const float* Up = pv.params + pv.off_up[l];
-    const float* Dn = pv.params + pv.off_down[l];
+    const int H = (int)pv.hidden, NC = H / kChunk;
+    const BwdSeq seq{&pv, NC};
     store_tile<M>(D.h, sm.xs, dh_store, kEmbed, 0);
     __syncthreads();
     FwdRegs<M> G;
     zero<M>(G.h);
-    for (int c = 0; c < H / kChunk; ++c) {
+    for (int c = 0; c < NC; ++c) {
+        const int s = 2 * (((int)pv.layers - 1 - l) * NC + c);
+        // the relu mask of this chunk, loaded before the GEMM issues its weight
+        // refills (vector memory counters complete in order)
+        typename S::Acc mask[S::RT][S::CT];
+        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+            mask[rt][ct][r] = v_tile[(size_t)row * H + kChunk * c + col];
+        });
         typename S::Acc v[S::RT][S::CT];
         zero<M>(v);
-        gemm_strip_t<M, kEmbed>(v, sm.xs, Dn + (size_t)kChunk * c * kEmbed, kEmbed, 32 * w);
+        ws.template gemm<0>(v, sm.xs, s, seq);
         __syncthreads();
         for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
-            const int hid = kChunk * c + col;
-            const float x = v_tile[(size_t)row * H + hid] > 0.0f ? v[rt][ct][r] : 0.0f;
+            const float x = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
             sm.vs[row * kLds + col] = x;
-            dv_store[(size_t)row * H + hid] = x;
+            dv_store[(size_t)row * H + kChunk * c + col] = x;
         });
         __syncthreads();
-        gemm_strip_t<M, kChunk>(G.h, sm.vs, Up + kChunk * c, H, 32 * w);
+        ws.template gemm<1>(G.h, sm.vs, s + 1, seq);
     }
     __syncthreads();
     bwd_layernorm<M>(sm, G, xn_tile, sd_tile, pv.params + pv.off_ln_gamma[l], tp + pv.off_ln_gamma[l],
@@ -174,6 +193,8 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
     const int tid = threadIdx.x;
     float* tp = ws.tp + (size_t)blockIdx.x * ws.tp_count;  // this tile's vector-parameter partials
 
+    WStream<M> wst;
+    fwd_start<M>(pv, wst);
     for (int idx = tid; idx < M * O; idx += 256) obsL[idx] = a.obs_slots[g0 * O + idx];
     __syncthreads();
 
@@ -183,8 +204,10 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
         fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l],
                          ws.xn + ((size_t)l * B + r0) * kEmbed, ws.sd + (size_t)l * B + r0,
                          ws.x + ((size_t)l * B + r0) * kEmbed);
-        fwd_block<M>(pv, l, sm, R, ws.v + ((size_t)l * B + r0) * H);
+        fwd_block<M>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H);
     }
+    // the backward's first weights are in flight through the final LN, the head and the loss
+    wst.start(2 * NL * (H / kChunk), BwdSeq{&pv, H / kChunk});
     fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[NL], pv.params + pv.off_ln_beta[NL],
                      ws.xn + ((size_t)NL * B + r0) * kEmbed, ws.sd + (size_t)NL * B + r0,
                      ws.x + ((size_t)NL * B + r0) * kEmbed);
@@ -285,7 +308,7 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
     bwd_layernorm<M>(sm, D, ws.xn + ((size_t)NL * B + r0) * kEmbed, ws.sd + (size_t)NL * B + r0,
                      pv.params + pv.off_ln_gamma[NL], tp + pv.off_ln_gamma[NL], tp + pv.off_ln_beta[NL], scratch);
     for (int l = NL - 1; l >= 0; --l) {
-        bwd_block<M>(pv, l, sm, D, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
+        bwd_block<M>(pv, l, sm, D, wst, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
                      ws.dhb + ((size_t)l * B + r0) * kEmbed, ws.xn + ((size_t)l * B + r0) * kEmbed,
                      ws.sd + (size_t)l * B + r0, tp, scratch);
     }
@@ -444,38 +467,120 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
     if (t == 0) a.normpart[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
 }
 
-// model/optimizer.metal:36-60; workgroup 0 also records the pre-clip norm.
-__global__ void __launch_bounds__(256) adam_kernel(float* __restrict__ param, const float* __restrict__ grad,
-                                                   float* __restrict__ mom, float* __restrict__ var,
-                                                   const float* __restrict__ normpart, uint32_t count, float lr,
-                                                   float beta1_pow, float beta2_pow, float max_grad_norm,
-                                                   float* __restrict__ mb_stats) {
+// The block matrices are contiguous from float_group: per block up [128 x H]
+// then down [H x 128]. Both matrix kinds split into (128 x H) / 4096 tiles of
+// 64 x 64; tile t's matrix, its row/column extents and the tile's origin.
+struct MatTile {
+    uint32_t base;  // arena offset of the matrix
+    uint32_t rows, cols;
+    uint32_t r0, c0;
+};
+__device__ __forceinline__ MatTile mat_tile(uint32_t t, uint32_t float_group, uint32_t H) {
+    const uint32_t per = H / 32;  // 64x64 tiles per matrix
+    const uint32_t mi = t / per, tt = t % per;
+    MatTile m;
+    m.base = float_group + mi * kEmbed * H;
+    m.rows = (mi & 1) ? H : kEmbed;
+    m.cols = (mi & 1) ? kEmbed : H;
+    m.r0 = (tt / (m.cols / 64)) * 64;
+    m.c0 = (tt % (m.cols / 64)) * 64;
+    return m;
+}
+constexpr int kTileLd = 65;  // LDS row stride of a 64 x 64 transpose tile
+
+// Writes the 64 x 64 tile held in lds ([r][c], stride kTileLd) transposed into
+// param_t: element (r0 + r, c0 + c) goes to base + (c0 + c) * rows + r0 + r.
+// Coalesced along r. Starts with a barrier.
+__device__ __forceinline__ void store_tile_t(const MatTile& m, const float* lds, float* param_t) {
+    __syncthreads();
+    const int t = threadIdx.x, r = t & 63;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int c = 4 * e + (t >> 6);
+        param_t[m.base + (size_t)(m.c0 + c) * m.rows + m.r0 + r] = lds[r * kTileLd + c];
+    }
+}
+
+// params_t from params (the transposed block matrices), one tile per workgroup.
+__global__ void __launch_bounds__(256) transpose_blocks_kernel(const float* __restrict__ param,
+                                                               float* __restrict__ param_t, uint32_t float_group,
+                                                               uint32_t H) {
+    __shared__ float lds[64 * kTileLd];
+    const MatTile m = mat_tile(blockIdx.x, float_group, H);
+    const int t = threadIdx.x, c = t & 63;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int r = 4 * e + (t >> 6);
+        lds[r * kTileLd + c] = param[m.base + (size_t)(m.r0 + r) * m.cols + m.c0 + c];
+    }
+    store_tile_t(m, lds, param_t);
+}
+
+struct AdamArgs {
+    float* param;
+    float* param_t;
+    const float* grad;
+    float* mom;
+    float* var;
+    const float* normpart;
+    float* mb_stats;
+    uint32_t count, float_group, off_head, hidden, mat_tiles;
+    float lr, beta1_pow, beta2_pow, max_grad_norm;
+};
+
+// model/optimizer.metal:36-60 for element i with the clip scale applied.
+__device__ __forceinline__ float adam_elem(const AdamArgs& a, uint32_t i, float scale) {
+    const float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f;
+    const float g = a.grad[i] * scale;
+    const float m = beta1 * a.mom[i] + (1.0f - beta1) * g;
+    const float v = beta2 * a.var[i] + (1.0f - beta2) * g * g;
+    a.mom[i] = m;
+    a.var[i] = v;
+    const float mHat = m / (1.0f - a.beta1_pow);
+    const float vHat = v / (1.0f - a.beta2_pow);
+    const float p = a.param[i] - a.lr * mHat / (sqrtf(vHat) + eps);
+    a.param[i] = p;
+    return p;
+}
+
+// Workgroups [0, mat_tiles) update one 64 x 64 block-matrix tile each and
+// write it transposed to param_t as well; the rest update the vector group and
+// the head elementwise. Workgroup 0 also records the pre-clip norm.
+__global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
+    __shared__ float lds[64 * kTileLd];
     // Every wave adds the kReduceBlocks partial norms in the same order, so all
     // workgroups see the same norm without synchronising with each other.
-    const int lane = threadIdx.x & 63;
+    const int t = threadIdx.x, lane = t & 63;
     float ns = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kReduceBlocks / 64; ++k) ns += normpart[lane + 64 * k];
+    for (int k = 0; k < kReduceBlocks / 64; ++k) ns += a.normpart[lane + 64 * k];
     const float norm = sqrtf(group_sum<64>(ns));
-    if (blockIdx.x == 0 && threadIdx.x == 0) mb_stats[5] = norm;
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= count) return;
-    const float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f;
-    const float scale = (max_grad_norm > 0.0f && norm > max_grad_norm) ? max_grad_norm / (norm + 1e-6f) : 1.0f;
-    const float g = grad[i] * scale;
-    const float m = beta1 * mom[i] + (1.0f - beta1) * g;
-    const float v = beta2 * var[i] + (1.0f - beta2) * g * g;
-    mom[i] = m;
-    var[i] = v;
-    const float mHat = m / (1.0f - beta1_pow);
-    const float vHat = v / (1.0f - beta2_pow);
-    param[i] = param[i] - lr * mHat / (sqrtf(vHat) + eps);
+    if (blockIdx.x == 0 && t == 0) a.mb_stats[5] = norm;
+    const float scale =
+        (a.max_grad_norm > 0.0f && norm > a.max_grad_norm) ? a.max_grad_norm / (norm + 1e-6f) : 1.0f;
+    if (blockIdx.x < a.mat_tiles) {
+        const MatTile m = mat_tile(blockIdx.x, a.float_group, a.hidden);
+        const int c = t & 63;
+#pragma unroll 4
+        for (int e = 0; e < 16; ++e) {
+            const int r = 4 * e + (t >> 6);
+            lds[r * kTileLd + c] = adam_elem(a, m.base + (m.r0 + r) * m.cols + m.c0 + c, scale);
+        }
+        store_tile_t(m, lds, a.param_t);
+        return;
+    }
+    const uint32_t j = (blockIdx.x - a.mat_tiles) * 256 + t;
+    const uint32_t i = j < a.float_group ? j : a.off_head + (j - a.float_group);
+    if (i < a.count) adam_elem(a, i, scale);
 }
 
 }  // namespace dev
 
 namespace {
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+// 64 x 64 tiles over all block matrices (each 128 x H or H x 128).
+uint32_t mat_tiles(const mg_policy_view& pv) { return 2 * pv.layers * (pv.hidden / 32); }
 
 struct WsPlan {
     size_t off[10];
@@ -528,6 +633,25 @@ int train_ws_bind(const mg_policy_view& pv, uint32_t rows, void* base, TrainWs* 
     ws->grad = (float*)(b + p.off[8]);
     ws->normpart = (float*)(b + p.off[9]);
     ws->tp_count = p.tp_count;
+    return MG_OK;
+}
+
+int check_matrix_layout(const mg_policy_view& pv) {
+    const uint32_t E = MG_EMBED, H = pv.hidden;
+    MG_CHECK(pv.embed == E && H % 64 == 0, MG_ERR_INVALID, "policy: embed 128 and hidden a multiple of 64 required");
+    for (uint32_t l = 0; l < pv.layers; ++l)
+        MG_CHECK(pv.off_up[l] == pv.float_group + 2 * l * E * H && pv.off_down[l] == pv.off_up[l] + E * H &&
+                     pv.off_head == pv.float_group + 2 * pv.layers * E * H,
+                 MG_ERR_INVALID, "policy: block matrices must be contiguous from float_group");
+    return MG_OK;
+}
+
+int launch_transpose_blocks(hipStream_t st, const mg_policy_view& pv) {
+    int rc = check_matrix_layout(pv);
+    if (rc) return rc;
+    hipLaunchKernelGGL(dev::transpose_blocks_kernel, dim3(mat_tiles(pv)), dim3(256), 0, st, pv.params, pv.params_t,
+                       pv.float_group, pv.hidden);
+    MG_HIP(hipGetLastError(), "transpose launch");
     return MG_OK;
 }
 
@@ -610,8 +734,25 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
     }
     {  // 4. Adam
         TimedLaunch tl(MG_K_ADAM, st);
-        hipLaunchKernelGGL(dev::adam_kernel, dim3((pv.count + 255) / 256), dim3(256), 0, st, pv.params, ws.grad, m, v,
-                           ws.normpart, pv.count, lr, step.beta1_pow, step.beta2_pow, hp.max_grad_norm, mb_stats);
+        dev::AdamArgs aa;
+        aa.param = pv.params;
+        aa.param_t = pv.params_t;
+        aa.grad = ws.grad;
+        aa.mom = m;
+        aa.var = v;
+        aa.normpart = ws.normpart;
+        aa.mb_stats = mb_stats;
+        aa.count = pv.count;
+        aa.float_group = pv.float_group;
+        aa.off_head = pv.off_head;
+        aa.hidden = H;
+        aa.mat_tiles = mat_tiles(pv);
+        aa.lr = lr;
+        aa.beta1_pow = step.beta1_pow;
+        aa.beta2_pow = step.beta2_pow;
+        aa.max_grad_norm = hp.max_grad_norm;
+        const uint32_t lin = pv.float_group + (pv.count - pv.off_head);
+        hipLaunchKernelGGL(dev::adam_kernel, dim3(aa.mat_tiles + (lin + 255) / 256), dim3(256), 0, st, aa);
         MG_HIP(hipGetLastError(), "adam launch");
     }
     return MG_OK;
