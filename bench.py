@@ -95,17 +95,22 @@ def bench_full(kernel, n, T, iters, O, A, epochs=4):
     model.collect()
     model.train(1)
     sync()
-    mg.timing_reset()
-    mg.timing_enable(True)
+    # throughput untimed (per-kernel events would add their own gaps), then one
+    # iteration with per-kernel events for the breakdown
     t0 = time.perf_counter()
     for _ in range(iters):
         model.collect()
         model.train(epochs)
     sync()
     dt = time.perf_counter() - t0
+    st = model.last_stats()
+    mg.timing_reset()
+    mg.timing_enable(True)
+    model.collect()
+    model.train(epochs)
+    sync()
     mg.timing_enable(False)
     times = mg.timing_get()
-    st = model.last_stats()
     B = min(n, 4096)
     out = {"env_steps_per_s": iters * n * T / dt, "s_per_iter": dt / iters,
            "minibatches_per_iter": epochs * T * n // B,

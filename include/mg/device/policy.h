@@ -1,19 +1,18 @@
 // Fused residual-MLP policy forward for a tile of M rows (M = 16, 32 or 64) on
-// one 256-thread workgroup, fp32 MFMA.
+// one workgroup of W waves (W = 4, or 8 for 16-row tiles), fp32 MFMA.
 //
 // Network (model/ppo.h:575-626): embed h = obs W_in + b_in; per block
 // h += relu(LN(h) Up) Down; final LN; head = LN(h) W_head (no bias).
 //
-// Mapping: wave w owns embed columns [32w, 32w + 32) of the residual stream h,
-// held in MFMA accumulator layout. 32- and 64-row tiles use
-// v_mfma_f32_32x32x2_f32 (one 32-column tile per wave); 16-row tiles use
-// v_mfma_f32_16x16x4_f32 (two 16-column tiles per wave), so a 4096-row
-// minibatch still spreads over 256 workgroups. Each block runs the hidden
-// dimension in 128-wide chunks so the hidden activations never leave the CU:
-// V_c = relu(x Up[:, c]) is computed by the four waves (32 hidden columns
-// each), staged in LDS, and immediately contracted with Down[c, :] into the
-// block output accumulator. LN outputs and hidden chunks are the A operands
-// (LDS, float4 reads); weights are the B operands, read straight from L2 (the
+// Mapping: wave w owns the 128 / W embed columns [SW w, SW w + SW) of the
+// residual stream h, held in MFMA accumulator layout. 32- and 64-row tiles use
+// v_mfma_f32_32x32x2_f32; 16-row tiles use v_mfma_f32_16x16x4_f32, so a
+// 4096-row minibatch still spreads over 256 workgroups. Each block runs the
+// hidden dimension in 128-wide chunks so the hidden activations never leave
+// the CU: V_c = relu(x Up[:, c]) is computed by all waves, staged in LDS, and
+// immediately contracted with Down[c, :] into the residual stream. LN outputs
+// and hidden chunks are the A operands (LDS, float4 reads); weights are the B
+// operands, streamed from L2 into registers one GEMM ahead of their use (the
 // whole 1 MB policy stays L2-resident across the grid).
 //
 // K-order permutation: with KS k-values per MFMA step, a k-group holds 4*KS
@@ -31,17 +30,21 @@ constexpr int kLds = kEmbed + 4;  // LDS row stride in floats (pad against bank 
 constexpr int kChunk = 128;       // hidden columns per chunk
 static_assert(kChunk == kEmbed, "every chunk GEMM contracts over 128");
 
-// MFMA shape used by an M-row tile.
-template <int M>
+// MFMA shape used by an M-row tile on W waves.
+template <int M, int W = 4>
 struct Shape {
+    static constexpr int NT = 64 * W;             // threads
+    static constexpr int SW = kEmbed / W;         // columns per wave
     static constexpr int MT = M >= 32 ? 32 : 16;  // MFMA M = N
     static constexpr int KS = MT == 32 ? 2 : 4;   // k per MFMA step
     static constexpr int KG = 4 * KS;             // k per float4 group
     static constexpr int RT = M / MT;             // row tiles
-    static constexpr int CT = 32 / MT;            // 32-column strips per wave, in MFMA tiles
+    static constexpr int CT = SW / MT;            // column tiles per wave
     static constexpr int REGS = MT == 32 ? 16 : 4;
     using Acc = typename std::conditional<MT == 32, f32x16, f32x4>::type;
     static_assert(M == 16 || M == 32 || M == 64, "tile rows");
+    static_assert(W == 4 || W == 8, "waves");
+    static_assert(SW % MT == 0, "a wave's strip holds whole MFMA tiles");
 
     __device__ static __forceinline__ Acc mfma(float a, float b, Acc c) {
         if constexpr (MT == 32)
@@ -67,25 +70,29 @@ struct FwdSmem {
 };
 
 // Residual stream of an M-row tile. Element (rt, ct, r) of wave w, lane l is
-// row MT rt + Shape::row(r, l), column 32 w + MT ct + l % MT.
-template <int M>
+// row MT rt + Shape::row(r, l), column SW w + MT ct + l % MT.
+template <int M, int W = 4>
 struct FwdRegs {
-    using S = Shape<M>;
+    using S = Shape<M, W>;
     typename S::Acc h[S::RT][S::CT];
 };
 
-template <int M>
-__device__ __forceinline__ void zero(typename Shape<M>::Acc (&a)[Shape<M>::RT][Shape<M>::CT]) {
+// A wave's accumulator tiles of an M-row tile.
+template <int M, int W = 4>
+using AccTile = typename Shape<M, W>::Acc[Shape<M, W>::RT][Shape<M, W>::CT];
+
+template <int M, int W = 4>
+__device__ __forceinline__ void zero(AccTile<M, W>& a) {
 #pragma unroll
-    for (int rt = 0; rt < Shape<M>::RT; ++rt)
+    for (int rt = 0; rt < Shape<M, W>::RT; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < Shape<M>::CT; ++ct) a[rt][ct] = typename Shape<M>::Acc{};
+        for (int ct = 0; ct < Shape<M, W>::CT; ++ct) a[rt][ct] = typename Shape<M, W>::Acc{};
 }
 
 // Calls f(rt, ct, r, row, col) for every accumulator element this thread holds.
-template <int M, class F>
+template <int M, int W = 4, class F>
 __device__ __forceinline__ void for_each_elem(F f) {
-    using S = Shape<M>;
+    using S = Shape<M, W>;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
 #pragma unroll
     for (int rt = 0; rt < S::RT; ++rt)
@@ -93,23 +100,23 @@ __device__ __forceinline__ void for_each_elem(F f) {
         for (int ct = 0; ct < S::CT; ++ct)
 #pragma unroll
             for (int r = 0; r < S::REGS; ++r)
-                f(rt, ct, r, S::MT * rt + S::row(r, lane), 32 * w + S::MT * ct + S::col(lane));
+                f(rt, ct, r, S::MT * rt + S::row(r, lane), S::SW * w + S::MT * ct + S::col(lane));
 }
 
 // B operand (weights) of NG k-groups of a 128-deep chunk GEMM for one wave's
-// 32-column strip, held in registers.
-template <int M, int NG>
+// strip, held in registers.
+template <int M, int W, int NG>
 struct BFrag {
-    float b[NG][Shape<M>::CT][4];
+    float b[NG][Shape<M, W>::CT][4];
 };
 
 // Loads k-groups [g0, g0 + NG) of a transposed weight operand: W^T element
 // (k, n) at wt_ptr[n * wt_ld + k], so each lane's four k-values are one
 // contiguous float4.
-template <int M, int NG>
-__device__ __forceinline__ void load_frag_t(BFrag<M, NG>& f, const float* wt_ptr, size_t wt_ld, int g0) {
-    using S = Shape<M>;
-    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane), n0 = 32 * (threadIdx.x >> 6);
+template <int M, int W, int NG>
+__device__ __forceinline__ void load_frag_t(BFrag<M, W, NG>& f, const float* wt_ptr, size_t wt_ld, int g0) {
+    using S = Shape<M, W>;
+    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane), n0 = S::SW * (threadIdx.x >> 6);
     const float* bp = wt_ptr + (size_t)(n0 + n) * wt_ld + 4 * q + S::KG * g0;
 #pragma unroll
     for (int g = 0; g < NG; ++g)
@@ -123,10 +130,9 @@ __device__ __forceinline__ void load_frag_t(BFrag<M, NG>& f, const float* wt_ptr
 
 // acc[rt][ct] += A[rows][k-groups g0 .. g0 + NG) @ B for this wave's strip. A
 // is in LDS (row stride kLds, A[m][k] at a_lds[m * kLds + k]).
-template <int M, int NG>
-__device__ __forceinline__ void gemm_frag(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
-                                          const float* a_lds, const BFrag<M, NG>& f, int g0) {
-    using S = Shape<M>;
+template <int M, int W, int NG>
+__device__ __forceinline__ void gemm_frag(AccTile<M, W>& acc, const float* a_lds, const BFrag<M, W, NG>& f, int g0) {
+    using S = Shape<M, W>;
     const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
     const float* ap = a_lds + n * kLds + 4 * q + S::KG * g0;
 #pragma unroll
@@ -155,16 +161,16 @@ struct FragSrc {
 // later GEMM's weights are issued as soon as registers free up, so their L2
 // latency overlaps the MFMA work (and the barriers) in between instead of
 // stalling every k-group.
-//  - 16-row tiles (one workgroup per CU, registers to spare): two whole
-//    fragments, one per GEMM role, each refilled two GEMMs ahead.
+//  - 16-row tiles (registers to spare): two whole fragments, one per GEMM
+//    role, each refilled two GEMMs ahead.
 //  - 32/64-row tiles (two workgroups per CU): the two halves of the current
 //    GEMM's fragment, each refilled with the next GEMM's half once consumed.
-template <int M>
+template <int M, int W = 4>
 struct WStream {
-    static constexpr int NGF = kEmbed / Shape<M>::KG;  // k-groups of one 128-deep GEMM
+    static constexpr int NGF = kEmbed / Shape<M, W>::KG;  // k-groups of one 128-deep GEMM
     static constexpr bool WHOLE = M == 16;
     static constexpr int NG = WHOLE ? NGF : NGF / 2;
-    BFrag<M, NG> b[2];
+    BFrag<M, W, NG> b[2];
     int total;  // GEMMs in the sequence
 
     template <class Src>
@@ -172,46 +178,45 @@ struct WStream {
         total = n;
         const FragSrc f0 = src(0);
         if constexpr (WHOLE) {
-            load_frag_t<M, NG>(b[0], f0.p, f0.ld, 0);
+            load_frag_t<M, W, NG>(b[0], f0.p, f0.ld, 0);
             if (n > 1) {
                 const FragSrc f1 = src(1);
-                load_frag_t<M, NG>(b[1], f1.p, f1.ld, 0);
+                load_frag_t<M, W, NG>(b[1], f1.p, f1.ld, 0);
             }
         } else {
-            load_frag_t<M, NG>(b[0], f0.p, f0.ld, 0);
-            load_frag_t<M, NG>(b[1], f0.p, f0.ld, NG);
+            load_frag_t<M, W, NG>(b[0], f0.p, f0.ld, 0);
+            load_frag_t<M, W, NG>(b[1], f0.p, f0.ld, NG);
         }
     }
 
     // acc += A @ W_s for the s-th GEMM of the sequence (ROLE = s & 1), then
     // refills the consumed registers.
     template <int ROLE, class Src>
-    __device__ __forceinline__ void gemm(typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
-                                         const float* a_lds, int s, Src src) {
+    __device__ __forceinline__ void gemm(AccTile<M, W>& acc, const float* a_lds, int s, Src src) {
         if constexpr (WHOLE) {
-            gemm_frag<M, NG>(acc, a_lds, b[ROLE], 0);
+            gemm_frag<M, W, NG>(acc, a_lds, b[ROLE], 0);
             if (s + 2 < total) {
                 const FragSrc f = src(s + 2);
-                load_frag_t<M, NG>(b[ROLE], f.p, f.ld, 0);
+                load_frag_t<M, W, NG>(b[ROLE], f.p, f.ld, 0);
             }
         } else {
             const bool more = s + 1 < total;
             FragSrc f{nullptr, 0};
             if (more) f = src(s + 1);
-            gemm_frag<M, NG>(acc, a_lds, b[0], 0);
-            if (more) load_frag_t<M, NG>(b[0], f.p, f.ld, 0);
-            gemm_frag<M, NG>(acc, a_lds, b[1], NG);
-            if (more) load_frag_t<M, NG>(b[1], f.p, f.ld, NG);
+            gemm_frag<M, W, NG>(acc, a_lds, b[0], 0);
+            if (more) load_frag_t<M, W, NG>(b[0], f.p, f.ld, 0);
+            gemm_frag<M, W, NG>(acc, a_lds, b[1], NG);
+            if (more) load_frag_t<M, W, NG>(b[1], f.p, f.ld, NG);
         }
     }
 };
 
 // Writes a register tile to LDS (row stride kLds) and optionally to global
 // memory (row stride ld), optionally through relu.
-template <int M, bool RELU = false>
-__device__ __forceinline__ void store_tile(const typename Shape<M>::Acc (&acc)[Shape<M>::RT][Shape<M>::CT],
-                                           float* lds, float* global = nullptr, size_t ld = 0, int gcol0 = 0) {
-    for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+template <int M, int W = 4, bool RELU = false>
+__device__ __forceinline__ void store_tile(const AccTile<M, W>& acc, float* lds, float* global = nullptr,
+                                           size_t ld = 0, int gcol0 = 0) {
+    for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
         float x = acc[rt][ct][r];
         if (RELU) x = x > 0.0f ? x : 0.0f;
         lds[row * kLds + col] = x;
@@ -221,14 +226,14 @@ __device__ __forceinline__ void store_tile(const typename Shape<M>::Acc (&acc)[S
 
 // model/input.metal:11-27: h = b_in + sum_k obs[k] W_in[k], in k order.
 // obsL is [M][O] in LDS.
-template <int M>
-__device__ __forceinline__ void fwd_embed(const mg_policy_view& pv, const float* obsL, int O, FwdRegs<M>& R) {
-    const float* W = pv.params + pv.off_in_w;
+template <int M, int W = 4>
+__device__ __forceinline__ void fwd_embed(const mg_policy_view& pv, const float* obsL, int O, FwdRegs<M, W>& R) {
+    const float* Win = pv.params + pv.off_in_w;
     const float* bias = pv.params + pv.off_in_b;
-    for_each_elem<M>([&](int rt, int ct, int r, int row, int col) { R.h[rt][ct][r] = bias[col]; });
+    for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) { R.h[rt][ct][r] = bias[col]; });
     for (int k = 0; k < O; ++k) {
-        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
-            R.h[rt][ct][r] += obsL[row * O + k] * W[k * kEmbed + col];
+        for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
+            R.h[rt][ct][r] += obsL[row * O + k] * Win[k * kEmbed + col];
         });
     }
 }
@@ -236,15 +241,16 @@ __device__ __forceinline__ void fwd_embed(const mg_policy_view& pv, const float*
 // model/layernorm.metal:10-71 on the register tile; the result goes to sm.xs.
 // If xn_out/sd_out/x_out are given, the normalised values, the standard
 // deviation and the output are also written there ([M][128], [M], [M][128],
-// row-major) for the backward pass.
-template <int M>
-__device__ __forceinline__ void fwd_layernorm(FwdSmem<M>& sm, const FwdRegs<M>& R, const float* gamma,
+// row-major; global memory or LDS) for the backward pass.
+template <int M, int W = 4>
+__device__ __forceinline__ void fwd_layernorm(FwdSmem<M>& sm, const FwdRegs<M, W>& R, const float* gamma,
                                               const float* beta, float* xn_out = nullptr, float* sd_out = nullptr,
                                               float* x_out = nullptr) {
-    constexpr int TPR = 256 / M;       // threads per row
-    constexpr int CPT = kEmbed / TPR;  // columns per thread
+    constexpr int TPR = Shape<M, W>::NT / M;  // threads per row
+    constexpr int CPT = kEmbed / TPR;         // columns per thread
+    static_assert(CPT % 4 == 0, "float4 columns");
     const int tid = threadIdx.x;
-    store_tile<M>(R.h, sm.xs);
+    store_tile<M, W>(R.h, sm.xs);
     __syncthreads();
     const int row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     float* xr = sm.xs + row * kLds + c0;
@@ -305,38 +311,39 @@ struct FwdSeq {
 // folded into the GEMM accumulator). xs holds LN(h); ws streams the forward
 // sequence (FwdSeq). If v_out is given, the relu'd hidden activations are
 // also written there ([M][hidden], row-major).
-template <int M>
-__device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M>& R,
-                                          WStream<M>& ws, float* v_out = nullptr) {
-    using S = Shape<M>;
+template <int M, int W = 4>
+__device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M, W>& R,
+                                          WStream<M, W>& ws, float* v_out = nullptr) {
+    using S = Shape<M, W>;
     const int H = (int)pv.hidden, NC = H / kChunk;
     const FwdSeq seq{&pv, NC};
     for (int c = 0; c < NC; ++c) {
         const int s = 2 * (l * NC + c);
         typename S::Acc v[S::RT][S::CT];
-        zero<M>(v);
+        zero<M, W>(v);
         ws.template gemm<0>(v, sm.xs, s, seq);
         __syncthreads();  // every wave is done reading the previous chunk from vs
-        store_tile<M, true>(v, sm.vs, v_out, H, kChunk * c);
+        store_tile<M, W, true>(v, sm.vs, v_out, H, kChunk * c);
         __syncthreads();
         ws.template gemm<1>(R.h, sm.vs, s + 1, seq);
     }
 }
 
 // Starts the forward GEMM sequence.
-template <int M>
-__device__ __forceinline__ void fwd_start(const mg_policy_view& pv, WStream<M>& ws) {
+template <int M, int W = 4>
+__device__ __forceinline__ void fwd_start(const mg_policy_view& pv, WStream<M, W>& ws) {
     const int NC = (int)pv.hidden / kChunk;
     ws.start(2 * (int)pv.layers * NC, FwdSeq{&pv, NC});
 }
 
 // model/linear.metal:17-37: head[row][j] = sum_k xs[row][k] W_head[k][j] for
-// j < HD, into headL ([M][HD] in LDS). Ends with a barrier.
-template <int M>
-__device__ __forceinline__ void fwd_head(const mg_policy_view& pv, FwdSmem<M>& sm, float* headL, int HD) {
-    constexpr int TPR = 256 / M, CPT = kEmbed / TPR;
+// j < HD, into headL ([M][HD] in LDS). Wh is W_head ([128][HD], global memory
+// or LDS). Ends with a barrier.
+template <int M, int W = 4>
+__device__ __forceinline__ void fwd_head(const float* Wh, FwdSmem<M>& sm, float* headL, int HD) {
+    constexpr int TPR = Shape<M, W>::NT / M, CPT = kEmbed / TPR;
     const int tid = threadIdx.x, row = tid / TPR, part = tid % TPR, c0 = part * CPT;
-    const float* Wh = pv.params + pv.off_head + c0 * HD;
+    const float* wp = Wh + c0 * HD;
     const float* xr = sm.xs + row * kLds + c0;
     float x[CPT];
 #pragma unroll
@@ -344,7 +351,7 @@ __device__ __forceinline__ void fwd_head(const mg_policy_view& pv, FwdSmem<M>& s
     for (int j = 0; j < HD; ++j) {
         float acc = 0.0f;
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) acc += x[c] * Wh[c * HD + j];
+        for (int c = 0; c < CPT; ++c) acc += x[c] * wp[c * HD + j];
         acc = group_sum<TPR>(acc);
         if (part == 0) headL[row * HD + j] = acc;
     }
@@ -352,18 +359,18 @@ __device__ __forceinline__ void fwd_head(const mg_policy_view& pv, FwdSmem<M>& s
 }
 
 // Whole forward: obs staged in obsL ([M][O], LDS) -> head in headL ([M][HD], LDS).
-template <int M>
-__device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem<M>& sm, FwdRegs<M>& R,
+template <int M, int W = 4>
+__device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem<M>& sm, FwdRegs<M, W>& R,
                                                const float* obsL, int O, float* headL, int HD) {
-    WStream<M> ws;
-    fwd_start<M>(pv, ws);
-    fwd_embed<M>(pv, obsL, O, R);
+    WStream<M, W> ws;
+    fwd_start<M, W>(pv, ws);
+    fwd_embed<M, W>(pv, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
-        fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l]);
-        fwd_block<M>(pv, (int)l, sm, R, ws);
+        fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l]);
+        fwd_block<M, W>(pv, (int)l, sm, R, ws);
     }
-    fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[pv.layers], pv.params + pv.off_ln_beta[pv.layers]);
-    fwd_head<M>(pv, sm, headL, HD);
+    fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[pv.layers], pv.params + pv.off_ln_beta[pv.layers]);
+    fwd_head<M, W>(pv.params + pv.off_head, sm, headL, HD);
 }
 
 }  // namespace dev

@@ -28,27 +28,38 @@ namespace mg {
 namespace dev {
 
 constexpr int kTR = kTileRows;  // rows per train_rows workgroup
+constexpr int kTW = 8;          // waves per train_rows workgroup (two per SIMD)
+constexpr int kTNT = 64 * kTW;  // threads per train_rows workgroup
 constexpr int kMaxHeadT = 64;
 constexpr int kMaxObsT = 64;
+using TS = Shape<kTR, kTW>;
+using TRegs = FwdRegs<kTR, kTW>;
+using TStream = WStream<kTR, kTW>;
 
 // Column sums over the tile's M rows: out[c * ostride] = sum_r a[r * lda + c] * b(r, c)
 // for the 128 embed columns, where b(r, c) is b[r * ldb + c] (ldb > 0), the
-// per-row scalar b[r * bstride] (ldb == 0), or 1 (b == nullptr). The two
-// halves of the workgroup sum half the rows each and are added in a fixed
-// order. `scratch` is 256 floats of LDS; ends with a barrier.
-template <int M>
+// per-row scalar b[r * bstride] (ldb == 0), or 1 (b == nullptr). The workgroup's
+// NT / 128 thread groups each sum a range of rows; the ranges are added in
+// order. `scratch` is NT floats of LDS; ends with a barrier.
+template <int M, int NT>
 __device__ __forceinline__ void tile_colsum(const float* a, int lda, const float* b, int ldb, int bstride,
                                             float* out, int ostride, float* scratch) {
-    const int t = threadIdx.x, c = t & 127, half = t >> 7;
+    constexpr int P = NT / kEmbed, RP = M / P;
+    const int t = threadIdx.x, c = t & (kEmbed - 1), part = t / kEmbed;
     float s = 0.0f;
 #pragma unroll
-    for (int r = half * (M / 2); r < (half + 1) * (M / 2); ++r) {
+    for (int r = part * RP; r < (part + 1) * RP; ++r) {
         const float x = a[r * lda + c];
         s += b ? x * (ldb ? b[r * ldb + c] : b[r * bstride]) : x;
     }
     scratch[t] = s;
     __syncthreads();
-    if (t < 128) out[c * ostride] = scratch[c] + scratch[128 + c];
+    if (t < kEmbed) {
+        float o = scratch[c];
+#pragma unroll
+        for (int p = 1; p < P; ++p) o += scratch[p * kEmbed + c];
+        out[c * ostride] = o;
+    }
     __syncthreads();
 }
 
@@ -66,13 +77,12 @@ struct RowsArgs {
     float* head_out;
 };
 
-// Gradient at the final LN output: dX = dZ W_head^T (model/linear.metal:40-60).
-template <int M>
-__device__ __forceinline__ void bwd_head(const mg_policy_view& pv, const float* dheadL, int HD, FwdRegs<M>& G) {
-    const float* Wh = pv.params + pv.off_head;
-    for_each_elem<M>([&](int rt, int ct, int r, int row, int col) { G.h[rt][ct][r] = 0.0f; });
+// Gradient at the final LN output: dX = dZ W_head^T (model/linear.metal:40-60);
+// Wh is W_head staged in LDS.
+__device__ __forceinline__ void bwd_head(const float* Wh, const float* dheadL, int HD, TRegs& G) {
+    for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) { G.h[rt][ct][r] = 0.0f; });
     for (int j = 0; j < HD; ++j) {
-        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+        for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
             G.h[rt][ct][r] += dheadL[row * HD + j] * Wh[col * HD + j];
         });
     }
@@ -80,17 +90,17 @@ __device__ __forceinline__ void bwd_head(const mg_policy_view& pv, const float* 
 
 // model/layernorm.metal:74-127 on a register tile: G holds the gradient at the
 // LN output on entry and the gradient at the LN input on exit. xn/sd are the
-// tile's forward captures. The tile's sums for dgamma (xn * dZ) and dbeta (dZ)
-// go to tp_gamma / tp_beta (the reference adds them with float atomics).
-template <int M>
-__device__ __forceinline__ void bwd_layernorm(FwdSmem<M>& sm, FwdRegs<M>& G, const float* xn, const float* sd,
+// tile's forward captures (LDS). The tile's sums for dgamma (xn * dZ) and
+// dbeta (dZ) go to tp_gamma / tp_beta (the reference adds them with float
+// atomics).
+__device__ __forceinline__ void bwd_layernorm(FwdSmem<kTR>& sm, TRegs& G, const float* xn, const float* sd,
                                               const float* gamma, float* tp_gamma, float* tp_beta, float* scratch) {
-    constexpr int TPR = 256 / M, CPT = kEmbed / TPR;
+    constexpr int TPR = kTNT / kTR, CPT = kEmbed / TPR;
     const int tid = threadIdx.x;
-    store_tile<M>(G.h, sm.xs);
+    store_tile<kTR, kTW>(G.h, sm.xs);
     __syncthreads();
-    tile_colsum<M>(sm.xs, kLds, xn, kEmbed, 0, tp_gamma, 1, scratch);
-    tile_colsum<M>(sm.xs, kLds, nullptr, 0, 0, tp_beta, 1, scratch);
+    tile_colsum<kTR, kTNT>(sm.xs, kLds, xn, kEmbed, 0, tp_gamma, 1, scratch);
+    tile_colsum<kTR, kTNT>(sm.xs, kLds, nullptr, 0, 0, tp_beta, 1, scratch);
     const int row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     float* zr = sm.xs + row * kLds + c0;
     const float* xr = xn + row * kEmbed + c0;
@@ -109,7 +119,8 @@ __device__ __forceinline__ void bwd_layernorm(FwdSmem<M>& sm, FwdRegs<M>& G, con
 #pragma unroll
     for (int c = 0; c < CPT; ++c) zr[c] = rd * (dxn[c] - r1 - xv[c] * r2);
     __syncthreads();
-    for_each_elem<M>([&](int rt, int ct, int r, int row2, int col) { G.h[rt][ct][r] = sm.xs[row2 * kLds + col]; });
+    for_each_elem<kTR, kTW>(
+        [&](int rt, int ct, int r, int row2, int col) { G.h[rt][ct][r] = sm.xs[row2 * kLds + col]; });
     __syncthreads();
 }
 
@@ -133,30 +144,29 @@ struct BwdSeq {
 // gradient at the block input. Chunked like the forward: dV_c = (dh Down_c^T)
 // masked by relu, then dx += dV_c Up_c^T; both weight reads are contiguous
 // float4s along the contraction; ws streams the backward sequence (BwdSeq).
-template <int M>
-__device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M>& D,
-                                          WStream<M>& ws, const float* v_tile, float* dv_store, float* dh_store,
-                                          const float* xn_tile, const float* sd_tile, float* tp, float* scratch) {
-    using S = Shape<M>;
+__device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSmem<kTR>& sm, TRegs& D,
+                                          TStream& ws, const float* v_tile, float* dv_store, float* dh_store,
+                                          const float* xn_tile, const float* sd_tile, const float* gamma,
+                                          float* tp, float* scratch) {
     const int H = (int)pv.hidden, NC = H / kChunk;
     const BwdSeq seq{&pv, NC};
-    store_tile<M>(D.h, sm.xs, dh_store, kEmbed, 0);
+    store_tile<kTR, kTW>(D.h, sm.xs, dh_store, kEmbed, 0);
     __syncthreads();
-    FwdRegs<M> G;
-    zero<M>(G.h);
+    TRegs G;
+    zero<kTR, kTW>(G.h);
     for (int c = 0; c < NC; ++c) {
         const int s = 2 * (((int)pv.layers - 1 - l) * NC + c);
         // the relu mask of this chunk, loaded before the GEMM issues its weight
         // refills (vector memory counters complete in order)
-        typename S::Acc mask[S::RT][S::CT];
-        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+        TS::Acc mask[TS::RT][TS::CT];
+        for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
             mask[rt][ct][r] = v_tile[(size_t)row * H + kChunk * c + col];
         });
-        typename S::Acc v[S::RT][S::CT];
-        zero<M>(v);
+        TS::Acc v[TS::RT][TS::CT];
+        zero<kTR, kTW>(v);
         ws.template gemm<0>(v, sm.xs, s, seq);
         __syncthreads();
-        for_each_elem<M>([&](int rt, int ct, int r, int row, int col) {
+        for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
             const float x = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
             sm.vs[row * kLds + col] = x;
             dv_store[(size_t)row * H + kChunk * c + col] = x;
@@ -165,24 +175,34 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSm
         ws.template gemm<1>(G.h, sm.vs, s + 1, seq);
     }
     __syncthreads();
-    bwd_layernorm<M>(sm, G, xn_tile, sd_tile, pv.params + pv.off_ln_gamma[l], tp + pv.off_ln_gamma[l],
-                     tp + pv.off_ln_beta[l], scratch);
+    bwd_layernorm(sm, G, xn_tile, sd_tile, gamma, tp + pv.off_ln_gamma[l], tp + pv.off_ln_beta[l], scratch);
 #pragma unroll
-    for (int rt = 0; rt < S::RT; ++rt)
+    for (int rt = 0; rt < TS::RT; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < S::CT; ++ct) D.h[rt][ct] = G.h[rt][ct] + D.h[rt][ct];  // residualAdd(dBranch, dStream)
+        for (int ct = 0; ct < TS::CT; ++ct) D.h[rt][ct] = G.h[rt][ct] + D.h[rt][ct];  // residualAdd(dBranch, dStream)
 }
 
-template <int M>
-__global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
-    __shared__ FwdSmem<M> sm;
-    __shared__ float obsL[M * kMaxObsT];
-    __shared__ float headL[M * kMaxHeadT];
-    __shared__ float dheadL[M * kMaxHeadT];
-    __shared__ float dlsL[M * kMaxHeadT];
-    __shared__ float statL[M * 5];
-    __shared__ float scratch[256];
-    FwdRegs<M> R;
+// LDS of one train_rows workgroup. The LN captures xn / sd are only read by
+// the LN backward, so they never leave the CU.
+struct RowsSmem {
+    FwdSmem<kTR> sm;
+    float xn[(MG_MAX_LAYERS + 1) * kTR * kEmbed];
+    float sd[(MG_MAX_LAYERS + 1) * kTR];
+    float ln[(MG_MAX_LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
+    float wh[kEmbed * kMaxHeadT];                // W_head
+    float obs[kTR * kMaxObsT];
+    float head[kTR * kMaxHeadT];
+    float dhead[kTR * kMaxHeadT];
+    float dls[kTR * kMaxHeadT];
+    float stat[kTR * 5];
+    float scratch[kTNT];
+};
+
+__global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
+    constexpr int M = kTR;
+    __shared__ RowsSmem L;
+    FwdSmem<M>& sm = L.sm;
+    TRegs R;
     const mg_policy_view& pv = a.pv;
     const TrainWs& ws = a.ws;
     const int O = (int)pv.obs_dim, A = (int)pv.act_dim, HD = (int)pv.head_dim, H = (int)pv.hidden;
@@ -193,34 +213,46 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
     const int tid = threadIdx.x;
     float* tp = ws.tp + (size_t)blockIdx.x * ws.tp_count;  // this tile's vector-parameter partials
 
-    WStream<M> wst;
-    fwd_start<M>(pv, wst);
-    for (int idx = tid; idx < M * O; idx += 256) obsL[idx] = a.obs_slots[g0 * O + idx];
+    // Everything small is loaded first, so waiting for it does not wait for the
+    // weight stream issued after it (vector memory counters complete in order).
+    for (int idx = tid; idx < M * O; idx += kTNT) L.obs[idx] = a.obs_slots[g0 * O + idx];
+    for (int idx = tid; idx < kEmbed * HD; idx += kTNT) L.wh[idx] = pv.params[pv.off_head + idx];
+    for (int idx = tid; idx < (NL + 1) * 2 * kEmbed; idx += kTNT) {
+        const int ln = idx / (2 * kEmbed), k = idx % (2 * kEmbed);
+        L.ln[idx] = k < kEmbed ? pv.params[pv.off_ln_gamma[ln] + k] : pv.params[pv.off_ln_beta[ln] + k - kEmbed];
+    }
+    // the loss inputs of this lane's row
+    float an = 0.0f, oldLp = 0.0f, ret = 0.0f;
+    int act = 0;
+    if (tid < M) {
+        const size_t gr = g0 + tid;
+        const float mean = a.adv_stats[2 * a.step.block], inv = a.adv_stats[2 * a.step.block + 1];
+        an = (a.adv_slots[gr] - mean) * inv;
+        oldLp = a.logp_slots[gr];
+        ret = a.ret_slots[gr];
+        if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
+    }
+    TStream wst;
+    fwd_start<M, kTW>(pv, wst);
     __syncthreads();
 
     // ---- forward with capture ----
-    fwd_embed<M>(pv, obsL, O, R);
+    fwd_embed<M, kTW>(pv, L.obs, O, R);
     for (int l = 0; l < NL; ++l) {
-        fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l],
-                         ws.xn + ((size_t)l * B + r0) * kEmbed, ws.sd + (size_t)l * B + r0,
-                         ws.x + ((size_t)l * B + r0) * kEmbed);
-        fwd_block<M>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H);
+        fwd_layernorm<M, kTW>(sm, R, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, L.xn + l * M * kEmbed,
+                              L.sd + l * M, ws.x + ((size_t)l * B + r0) * kEmbed);
+        fwd_block<M, kTW>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H);
     }
     // the backward's first weights are in flight through the final LN, the head and the loss
     wst.start(2 * NL * (H / kChunk), BwdSeq{&pv, H / kChunk});
-    fwd_layernorm<M>(sm, R, pv.params + pv.off_ln_gamma[NL], pv.params + pv.off_ln_beta[NL],
-                     ws.xn + ((size_t)NL * B + r0) * kEmbed, ws.sd + (size_t)NL * B + r0,
-                     ws.x + ((size_t)NL * B + r0) * kEmbed);
-    fwd_head<M>(pv, sm, headL, HD);
+    fwd_layernorm<M, kTW>(sm, R, L.ln + NL * 2 * kEmbed, L.ln + NL * 2 * kEmbed + kEmbed, L.xn + NL * M * kEmbed,
+                          L.sd + NL * M, ws.x + ((size_t)NL * B + r0) * kEmbed);
+    fwd_head<M, kTW>(L.wh, sm, L.head, HD);
 
     // ---- loss and head gradient, one lane per row ----
     if (tid < M) {
-        const float* h = headL + tid * HD;
-        float* dz = dheadL + tid * HD;
-        const size_t gr = g0 + tid;
-        const float mean = a.adv_stats[2 * a.step.block], inv = a.adv_stats[2 * a.step.block + 1];
-        const float an = (a.adv_slots[gr] - mean) * inv;
-        const float oldLp = a.logp_slots[gr];
+        const float* h = L.head + tid * HD;
+        float* dz = L.dhead + tid * HD;
         const float scale = 1.0f / (float)B;
         const float clip = a.hp.clip, ec = a.hp.entropy_coef;
         float entropy = 0.0f, logpA, ratio, gLogp, policyLoss;
@@ -234,7 +266,6 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
                 const float lp = h[j] - lse;
                 entropy -= mg::expf(lp) * lp;
             }
-            const int act = static_cast<const int*>(a.action_slots)[gr];
             logpA = h[act] - lse;
             ratio = mg::expf(logpA - oldLp);
             const float surr1 = ratio * an;
@@ -249,12 +280,12 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
                 dz[j] = g * scale;
             }
         } else {  // model/gaussian.metal:76-135
-            const float* act = static_cast<const float*>(a.action_slots) + gr * A;
+            const float* actg = static_cast<const float*>(a.action_slots) + (g0 + tid) * A;
             const float* logStd = pv.params + pv.off_log_std;
             float logp = 0.0f;
             for (int k = 0; k < A; ++k) {
                 const float ls = logStd[k];
-                const float d = (act[k] - h[k]) * mg::expf(-ls);
+                const float d = (actg[k] - h[k]) * mg::expf(-ls);
                 logp += -0.5f * d * d - ls - kLogSqrt2Pi;
                 entropy += ls + kLogSqrt2Pi + 0.5f;
             }
@@ -268,14 +299,14 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
             for (int k = 0; k < A; ++k) {
                 const float ls = logStd[k];
                 const float invStd = mg::expf(-ls);
-                const float d = (act[k] - h[k]) * invStd;
+                const float d = (actg[k] - h[k]) * invStd;
                 dz[k] = gLogp * d * invStd * scale;
-                dlsL[tid * A + k] = (gLogp * (d * d - 1.0f) - ec) * scale;
+                L.dls[tid * A + k] = (gLogp * (d * d - 1.0f) - ec) * scale;
             }
         }
-        const float vErr = h[A] - a.ret_slots[gr];
+        const float vErr = h[A] - ret;
         dz[A] = a.hp.value_coef * vErr * scale;
-        float* st = statL + tid * 5;
+        float* st = L.stat + tid * 5;
         st[0] = policyLoss;
         st[1] = 0.5f * a.hp.value_coef * vErr * vErr;
         st[2] = entropy;
@@ -289,35 +320,35 @@ __global__ void __launch_bounds__(256) train_rows_kernel(const RowsArgs a) {
     // model/linear.metal:71-93 on this tile: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
     // (sm.xs still holds the final LN output x_f)
     for (int j = 0; j < HD; ++j)
-        tile_colsum<M>(sm.xs, kLds, dheadL + j, 0, HD, tp + pv.float_group + j, HD, scratch);
+        tile_colsum<M, kTNT>(sm.xs, kLds, L.dhead + j, 0, HD, tp + pv.float_group + j, HD, L.scratch);
     if (pv.continuous && tid < A) {  // model/gaussian.metal:166-168, summed over the tile in row order
         float s = 0.0f;
-        for (int r = 0; r < M; ++r) s += dlsL[r * A + tid];
+        for (int r = 0; r < M; ++r) s += L.dls[r * A + tid];
         tp[pv.off_log_std + tid] = s;
     }
     if (tid >= 64 && tid < 64 + 5) {  // the tile's LossStats sums, in row order
         const int q = tid - 64;
         float s = 0.0f;
-        for (int r = 0; r < M; ++r) s += statL[r * 5 + q];
+        for (int r = 0; r < M; ++r) s += L.stat[r * 5 + q];
         tp[pv.float_group + kEmbed * HD + q] = s;
     }
 
     // ---- backward ----
-    FwdRegs<M> D;
-    bwd_head<M>(pv, dheadL, HD, D);
-    bwd_layernorm<M>(sm, D, ws.xn + ((size_t)NL * B + r0) * kEmbed, ws.sd + (size_t)NL * B + r0,
-                     pv.params + pv.off_ln_gamma[NL], tp + pv.off_ln_gamma[NL], tp + pv.off_ln_beta[NL], scratch);
+    TRegs D;
+    bwd_head(L.wh, L.dhead, HD, D);
+    bwd_layernorm(sm, D, L.xn + NL * M * kEmbed, L.sd + NL * M, L.ln + NL * 2 * kEmbed, tp + pv.off_ln_gamma[NL],
+                  tp + pv.off_ln_beta[NL], L.scratch);
     for (int l = NL - 1; l >= 0; --l) {
-        bwd_block<M>(pv, l, sm, D, wst, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
-                     ws.dhb + ((size_t)l * B + r0) * kEmbed, ws.xn + ((size_t)l * B + r0) * kEmbed,
-                     ws.sd + (size_t)l * B + r0, tp, scratch);
+        bwd_block(pv, l, sm, D, wst, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
+                  ws.dhb + ((size_t)l * B + r0) * kEmbed, L.xn + l * M * kEmbed, L.sd + l * M,
+                  L.ln + l * 2 * kEmbed, tp, L.scratch);
     }
     // model/input.metal:38-60 on this tile: dW_in[k][c] = sum_r obs[r][k] dh0[r][c], db_in = sum_r dh0
-    store_tile<M>(D.h, sm.xs);
+    store_tile<M, kTW>(D.h, sm.xs);
     __syncthreads();
-    tile_colsum<M>(sm.xs, kLds, nullptr, 0, 0, tp + pv.off_in_b, 1, scratch);
+    tile_colsum<M, kTNT>(sm.xs, kLds, nullptr, 0, 0, tp + pv.off_in_b, 1, L.scratch);
     for (int k = 0; k < O; ++k)
-        tile_colsum<M>(sm.xs, kLds, obsL + k, 0, O, tp + pv.off_in_w + k * kEmbed, 1, scratch);
+        tile_colsum<M, kTNT>(sm.xs, kLds, L.obs + k, 0, O, tp + pv.off_in_w + k * kEmbed, 1, L.scratch);
 }
 
 // ---- weight gradients ---------------------------------------------------------
@@ -433,8 +464,17 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
         for (uint32_t c0 = blockIdx.x * 64; c0 < stat0 + 5; c0 += a.small_wgs * 64) {
             const uint32_t col = c0 + (t & 63);
             float s = 0.0f;
-            if (col < stat0 + 5)
-                for (uint32_t k = grp * per; k < (grp + 1) * per; ++k) s += a.tp[(size_t)k * a.tp_count + col];
+            if (col < stat0 + 5) {
+                const float* src = a.tp + (size_t)grp * per * a.tp_count + col;
+                // loads issued eight at a time, added in tile order
+                for (uint32_t k0 = 0; k0 < per; k0 += 8) {
+                    float x[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) x[u] = k0 + u < per ? src[(size_t)(k0 + u) * a.tp_count] : 0.0f;
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) s += x[u];
+                }
+            }
             part[grp][t & 63] = s;
             __syncthreads();
             if (t < 64 && col < stat0 + 5) {
@@ -454,8 +494,12 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
     } else {
         const uint32_t nw = gridDim.x - a.small_wgs;
         for (uint32_t i = a.float_group + (blockIdx.x - a.small_wgs) * 256 + t; i < a.off_head; i += nw * 256) {
+            float x[kSplits];
+#pragma unroll
+            for (int s = 0; s < kSplits; ++s) x[s] = s < (int)a.splits ? a.partial[(size_t)s * a.count + i] : 0.0f;
             float g = 0.0f;
-            for (uint32_t s = 0; s < a.splits; ++s) g += a.partial[(size_t)s * a.count + i];
+#pragma unroll
+            for (int s = 0; s < kSplits; ++s) g += x[s];
             a.grad[i] = g;
             sq += g * g;
         }
@@ -468,35 +512,36 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
 }
 
 // The block matrices are contiguous from float_group: per block up [128 x H]
-// then down [H x 128]. Both matrix kinds split into (128 x H) / 4096 tiles of
-// 64 x 64; tile t's matrix, its row/column extents and the tile's origin.
+// then down [H x 128]. Both matrix kinds split into (128 x H) / 1024 tiles of
+// 32 x 32; tile t's matrix, its row/column extents and the tile's origin.
+constexpr int kTT = 32;  // transpose tile edge
 struct MatTile {
     uint32_t base;  // arena offset of the matrix
     uint32_t rows, cols;
     uint32_t r0, c0;
 };
 __device__ __forceinline__ MatTile mat_tile(uint32_t t, uint32_t float_group, uint32_t H) {
-    const uint32_t per = H / 32;  // 64x64 tiles per matrix
+    const uint32_t per = H * kEmbed / (kTT * kTT);  // tiles per matrix
     const uint32_t mi = t / per, tt = t % per;
     MatTile m;
     m.base = float_group + mi * kEmbed * H;
     m.rows = (mi & 1) ? H : kEmbed;
     m.cols = (mi & 1) ? kEmbed : H;
-    m.r0 = (tt / (m.cols / 64)) * 64;
-    m.c0 = (tt % (m.cols / 64)) * 64;
+    m.r0 = (tt / (m.cols / kTT)) * kTT;
+    m.c0 = (tt % (m.cols / kTT)) * kTT;
     return m;
 }
-constexpr int kTileLd = 65;  // LDS row stride of a 64 x 64 transpose tile
+constexpr int kTileLd = kTT + 1;  // LDS row stride of a transpose tile
 
-// Writes the 64 x 64 tile held in lds ([r][c], stride kTileLd) transposed into
+// Writes the tile held in lds ([r][c], stride kTileLd) transposed into
 // param_t: element (r0 + r, c0 + c) goes to base + (c0 + c) * rows + r0 + r.
 // Coalesced along r. Starts with a barrier.
 __device__ __forceinline__ void store_tile_t(const MatTile& m, const float* lds, float* param_t) {
     __syncthreads();
-    const int t = threadIdx.x, r = t & 63;
+    const int t = threadIdx.x, r = t & (kTT - 1);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int c = 4 * e + (t >> 6);
+    for (int e = 0; e < kTT * kTT / 256; ++e) {
+        const int c = (256 / kTT) * e + t / kTT;
         param_t[m.base + (size_t)(m.c0 + c) * m.rows + m.r0 + r] = lds[r * kTileLd + c];
     }
 }
@@ -505,12 +550,12 @@ __device__ __forceinline__ void store_tile_t(const MatTile& m, const float* lds,
 __global__ void __launch_bounds__(256) transpose_blocks_kernel(const float* __restrict__ param,
                                                                float* __restrict__ param_t, uint32_t float_group,
                                                                uint32_t H) {
-    __shared__ float lds[64 * kTileLd];
+    __shared__ float lds[kTT * kTileLd];
     const MatTile m = mat_tile(blockIdx.x, float_group, H);
-    const int t = threadIdx.x, c = t & 63;
+    const int t = threadIdx.x, c = t & (kTT - 1);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int r = 4 * e + (t >> 6);
+    for (int e = 0; e < kTT * kTT / 256; ++e) {
+        const int r = (256 / kTT) * e + t / kTT;
         lds[r * kTileLd + c] = param[m.base + (size_t)(m.r0 + r) * m.cols + m.c0 + c];
     }
     store_tile_t(m, lds, param_t);
@@ -543,11 +588,11 @@ __device__ __forceinline__ float adam_elem(const AdamArgs& a, uint32_t i, float 
     return p;
 }
 
-// Workgroups [0, mat_tiles) update one 64 x 64 block-matrix tile each and
+// Workgroups [0, mat_tiles) update one 32 x 32 block-matrix tile each and
 // write it transposed to param_t as well; the rest update the vector group and
 // the head elementwise. Workgroup 0 also records the pre-clip norm.
 __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
-    __shared__ float lds[64 * kTileLd];
+    __shared__ float lds[kTT * kTileLd];
     // Every wave adds the kReduceBlocks partial norms in the same order, so all
     // workgroups see the same norm without synchronising with each other.
     const int t = threadIdx.x, lane = t & 63;
@@ -560,10 +605,10 @@ __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
         (a.max_grad_norm > 0.0f && norm > a.max_grad_norm) ? a.max_grad_norm / (norm + 1e-6f) : 1.0f;
     if (blockIdx.x < a.mat_tiles) {
         const MatTile m = mat_tile(blockIdx.x, a.float_group, a.hidden);
-        const int c = t & 63;
-#pragma unroll 4
-        for (int e = 0; e < 16; ++e) {
-            const int r = 4 * e + (t >> 6);
+        const int c = t & (kTT - 1);
+#pragma unroll
+        for (int e = 0; e < kTT * kTT / 256; ++e) {
+            const int r = (256 / kTT) * e + t / kTT;
             lds[r * kTileLd + c] = adam_elem(a, m.base + (m.r0 + r) * m.cols + m.c0 + c, scale);
         }
         store_tile_t(m, lds, a.param_t);
@@ -579,11 +624,11 @@ __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
 namespace {
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// 64 x 64 tiles over all block matrices (each 128 x H or H x 128).
-uint32_t mat_tiles(const mg_policy_view& pv) { return 2 * pv.layers * (pv.hidden / 32); }
+// 32 x 32 tiles over all block matrices (each 128 x H or H x 128).
+uint32_t mat_tiles(const mg_policy_view& pv) { return 2 * pv.layers * (pv.hidden * MG_EMBED / 1024); }
 
 struct WsPlan {
-    size_t off[10];
+    size_t off[8];
     size_t total;
     uint32_t tp_count;
 };
@@ -592,10 +637,8 @@ WsPlan plan(const mg_policy_view& pv, uint32_t B) {
     const size_t E = MG_EMBED, L = pv.layers, H = pv.hidden, HD = pv.head_dim;
     WsPlan p;
     p.tp_count = (uint32_t)align256(pv.float_group + E * HD + 5);
-    const size_t sizes[10] = {
-        (L + 1) * B * E * 4,                       // xn
+    const size_t sizes[8] = {
         (L + 1) * B * E * 4,                       // x
-        (L + 1) * B * 4,                           // sd
         L * B * H * 4,                             // v
         L * B * E * 4,                             // dhb
         L * B * H * 4,                             // dvb
@@ -605,7 +648,7 @@ WsPlan plan(const mg_policy_view& pv, uint32_t B) {
         (size_t)kReduceBlocks * 4,                 // normpart
     };
     size_t o = 0;
-    for (int k = 0; k < 10; ++k) {
+    for (int k = 0; k < 8; ++k) {
         p.off[k] = o;
         o += align256(sizes[k]);
     }
@@ -622,16 +665,14 @@ int train_ws_bytes(const mg_policy_view& pv, uint32_t rows, size_t* bytes) {
 int train_ws_bind(const mg_policy_view& pv, uint32_t rows, void* base, TrainWs* ws) {
     WsPlan p = plan(pv, rows);
     char* b = static_cast<char*>(base);
-    ws->xn = (float*)(b + p.off[0]);
-    ws->x = (float*)(b + p.off[1]);
-    ws->sd = (float*)(b + p.off[2]);
-    ws->v = (float*)(b + p.off[3]);
-    ws->dhb = (float*)(b + p.off[4]);
-    ws->dvb = (float*)(b + p.off[5]);
-    ws->tp = (float*)(b + p.off[6]);
-    ws->partial = (float*)(b + p.off[7]);
-    ws->grad = (float*)(b + p.off[8]);
-    ws->normpart = (float*)(b + p.off[9]);
+    ws->x = (float*)(b + p.off[0]);
+    ws->v = (float*)(b + p.off[1]);
+    ws->dhb = (float*)(b + p.off[2]);
+    ws->dvb = (float*)(b + p.off[3]);
+    ws->tp = (float*)(b + p.off[4]);
+    ws->partial = (float*)(b + p.off[5]);
+    ws->grad = (float*)(b + p.off[6]);
+    ws->normpart = (float*)(b + p.off[7]);
     ws->tp_count = p.tp_count;
     return MG_OK;
 }
@@ -683,7 +724,7 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         ra.logp_slots = logp_slots;
         ra.adv_stats = adv_stats;
         ra.head_out = head_out;
-        hipLaunchKernelGGL((dev::train_rows_kernel<dev::kTR>), dim3(B / dev::kTR), dim3(256), 0, st, ra);
+        hipLaunchKernelGGL(dev::train_rows_kernel, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         MG_HIP(hipGetLastError(), "train rows launch");
     }
     {  // 2. block-matrix weight gradients
