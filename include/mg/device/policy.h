@@ -63,10 +63,13 @@ struct Shape {
     __device__ static __forceinline__ int quad(int lane) { return lane / MT; }
 };
 
-template <int M>
+// NV = 2 double-buffers the hidden chunk: chunk c writes vs[c & 1], so the
+// write never races the previous chunk's readers and one barrier per chunk
+// suffices.
+template <int M, int NV = 1>
 struct FwdSmem {
-    float xs[M * kLds];  // LN output (A operand of the up GEMM)
-    float vs[M * kLds];  // relu'd hidden chunk (A operand of the down GEMM)
+    float xs[M * kLds];      // LN output (A operand of the up GEMM)
+    float vs[NV][M * kLds];  // relu'd hidden chunk (A operand of the down GEMM)
 };
 
 // Residual stream of an M-row tile. Element (rt, ct, r) of wave w, lane l is
@@ -135,19 +138,22 @@ __device__ __forceinline__ void gemm_frag(AccTile<M, W>& acc, const float* a_lds
     using S = Shape<M, W>;
     const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
     const float* ap = a_lds + n * kLds + 4 * q + S::KG * g0;
+    // the whole A operand first (one LDS latency per GEMM instead of one per
+    // k-group pair), then the MFMAs back to back
+    f32x4 a[NG][S::RT];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        f32x4 a[S::RT];
+    for (int g = 0; g < NG; ++g)
 #pragma unroll
         for (int rt = 0; rt < S::RT; ++rt)
-            a[rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
+            a[g][rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int rt = 0; rt < S::RT; ++rt)
 #pragma unroll
-                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[rt][j], f.b[g][ct][j], acc[rt][ct]);
-    }
+                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[g][rt][j], f.b[g][ct][j], acc[rt][ct]);
 }
 
 // Where the s-th weight operand of a GEMM sequence lives (transposed layout).
@@ -160,7 +166,11 @@ struct FragSrc {
 // operands are known in advance (a forward or backward pass). The loads of a
 // later GEMM's weights are issued as soon as registers free up, so their L2
 // latency overlaps the MFMA work (and the barriers) in between instead of
-// stalling every k-group.
+// stalling every k-group. With whole fragments every GEMM issues the same
+// loads on every path (past the end of the sequence it reloads its own
+// operand): the compiler's vector-memory wait counts are then exact at the
+// chunk loop's head instead of the conservative merge of paths with different
+// numbers of loads in flight.
 //  - 16-row tiles (registers to spare): two whole fragments, one per GEMM
 //    role, each refilled two GEMMs ahead.
 //  - 32/64-row tiles (two workgroups per CU): the two halves of the current
@@ -173,16 +183,15 @@ struct WStream {
     BFrag<M, W, NG> b[2];
     int total;  // GEMMs in the sequence
 
+    // n >= 2 GEMMs (a block has two per chunk).
     template <class Src>
     __device__ __forceinline__ void start(int n, Src src) {
         total = n;
         const FragSrc f0 = src(0);
         if constexpr (WHOLE) {
+            const FragSrc f1 = src(1);
             load_frag_t<M, W, NG>(b[0], f0.p, f0.ld, 0);
-            if (n > 1) {
-                const FragSrc f1 = src(1);
-                load_frag_t<M, W, NG>(b[1], f1.p, f1.ld, 0);
-            }
+            load_frag_t<M, W, NG>(b[1], f1.p, f1.ld, 0);
         } else {
             load_frag_t<M, W, NG>(b[0], f0.p, f0.ld, 0);
             load_frag_t<M, W, NG>(b[1], f0.p, f0.ld, NG);
@@ -194,11 +203,9 @@ struct WStream {
     template <int ROLE, class Src>
     __device__ __forceinline__ void gemm(AccTile<M, W>& acc, const float* a_lds, int s, Src src) {
         if constexpr (WHOLE) {
+            const FragSrc f = src(s + 2 < total ? s + 2 : s);
             gemm_frag<M, W, NG>(acc, a_lds, b[ROLE], 0);
-            if (s + 2 < total) {
-                const FragSrc f = src(s + 2);
-                load_frag_t<M, W, NG>(b[ROLE], f.p, f.ld, 0);
-            }
+            load_frag_t<M, W, NG>(b[ROLE], f.p, f.ld, 0);
         } else {
             const bool more = s + 1 < total;
             FragSrc f{nullptr, 0};
@@ -211,17 +218,38 @@ struct WStream {
     }
 };
 
-// Writes a register tile to LDS (row stride kLds) and optionally to global
-// memory (row stride ld), optionally through relu.
+// Writes a register tile to LDS (row stride kLds), optionally through relu.
 template <int M, int W = 4, bool RELU = false>
-__device__ __forceinline__ void store_tile(const AccTile<M, W>& acc, float* lds, float* global = nullptr,
-                                           size_t ld = 0, int gcol0 = 0) {
+__device__ __forceinline__ void store_tile(const AccTile<M, W>& acc, float* lds) {
     for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
         float x = acc[rt][ct][r];
         if (RELU) x = x > 0.0f ? x : 0.0f;
         lds[row * kLds + col] = x;
-        if (global) global[(size_t)row * ld + gcol0 + col] = x;
     });
+}
+
+// The same, and also to global memory at global[row * ld + gcol0 + col].
+template <int M, int W = 4, bool RELU = false>
+__device__ __forceinline__ void store_tile_g(const AccTile<M, W>& acc, float* lds, float* global, size_t ld,
+                                             int gcol0) {
+    for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
+        float x = acc[rt][ct][r];
+        if (RELU) x = x > 0.0f ? x : 0.0f;
+        lds[row * kLds + col] = x;
+        global[(size_t)row * ld + gcol0 + col] = x;
+    });
+}
+
+// Copies an LDS tile ([M][128], row stride kLds) to global memory
+// (global[row * ld + col]) as float4 rows, NT threads.
+template <int M, int NT>
+__device__ __forceinline__ void copy_rows_g(const float* lds, float* global, size_t ld) {
+#pragma unroll
+    for (int i = threadIdx.x; i < M * kEmbed / 4; i += NT) {
+        const int row = i / (kEmbed / 4), c4 = 4 * (i % (kEmbed / 4));
+        *reinterpret_cast<f32x4*>(global + (size_t)row * ld + c4) =
+            *reinterpret_cast<const f32x4*>(lds + row * kLds + c4);
+    }
 }
 
 // model/input.metal:11-27: h = b_in + sum_k obs[k] W_in[k], in k order.
@@ -242,8 +270,8 @@ __device__ __forceinline__ void fwd_embed(const mg_policy_view& pv, const float*
 // If xn_out/sd_out/x_out are given, the normalised values, the standard
 // deviation and the output are also written there ([M][128], [M], [M][128],
 // row-major; global memory or LDS) for the backward pass.
-template <int M, int W = 4>
-__device__ __forceinline__ void fwd_layernorm(FwdSmem<M>& sm, const FwdRegs<M, W>& R, const float* gamma,
+template <int M, int W = 4, int NV = 1>
+__device__ __forceinline__ void fwd_layernorm(FwdSmem<M, NV>& sm, const FwdRegs<M, W>& R, const float* gamma,
                                               const float* beta, float* xn_out = nullptr, float* sd_out = nullptr,
                                               float* x_out = nullptr) {
     constexpr int TPR = Shape<M, W>::NT / M;  // threads per row
@@ -309,23 +337,25 @@ struct FwdSeq {
 // h += relu(xs Up) Down, the hidden dimension in 128-wide chunks whose Down
 // products accumulate straight into the residual stream (the residual add
 // folded into the GEMM accumulator). xs holds LN(h); ws streams the forward
-// sequence (FwdSeq). If v_out is given, the relu'd hidden activations are
-// also written there ([M][hidden], row-major).
-template <int M, int W = 4>
-__device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M>& sm, FwdRegs<M, W>& R,
+// sequence (FwdSeq). With VOUT the relu'd hidden activations are also written
+// to v_out ([M][hidden], row-major).
+template <int M, int W = 4, bool VOUT = false, int NV = 1>
+__device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M, NV>& sm, FwdRegs<M, W>& R,
                                           WStream<M, W>& ws, float* v_out = nullptr) {
     using S = Shape<M, W>;
     const int H = (int)pv.hidden, NC = H / kChunk;
     const FwdSeq seq{&pv, NC};
     for (int c = 0; c < NC; ++c) {
         const int s = 2 * (l * NC + c);
+        float* vs = sm.vs[NV == 2 ? (c & 1) : 0];
         typename S::Acc v[S::RT][S::CT];
         zero<M, W>(v);
         ws.template gemm<0>(v, sm.xs, s, seq);
-        __syncthreads();  // every wave is done reading the previous chunk from vs
-        store_tile<M, W, true>(v, sm.vs, v_out, H, kChunk * c);
+        if constexpr (NV == 1) __syncthreads();  // every wave is done reading the previous chunk from vs
+        store_tile<M, W, true>(v, vs);
         __syncthreads();
-        ws.template gemm<1>(R.h, sm.vs, s + 1, seq);
+        if constexpr (VOUT) copy_rows_g<M, S::NT>(vs, v_out + kChunk * c, H);
+        ws.template gemm<1>(R.h, vs, s + 1, seq);
     }
 }
 
@@ -339,8 +369,8 @@ __device__ __forceinline__ void fwd_start(const mg_policy_view& pv, WStream<M, W
 // model/linear.metal:17-37: head[row][j] = sum_k xs[row][k] W_head[k][j] for
 // j < HD, into headL ([M][HD] in LDS). Wh is W_head ([128][HD], global memory
 // or LDS). Ends with a barrier.
-template <int M, int W = 4>
-__device__ __forceinline__ void fwd_head(const float* Wh, FwdSmem<M>& sm, float* headL, int HD) {
+template <int M, int W = 4, int NV = 1>
+__device__ __forceinline__ void fwd_head(const float* Wh, FwdSmem<M, NV>& sm, float* headL, int HD) {
     constexpr int TPR = Shape<M, W>::NT / M, CPT = kEmbed / TPR;
     const int tid = threadIdx.x, row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     const float* wp = Wh + c0 * HD;

@@ -35,6 +35,7 @@ constexpr int kMaxObsT = 64;
 using TS = Shape<kTR, kTW>;
 using TRegs = FwdRegs<kTR, kTW>;
 using TStream = WStream<kTR, kTW>;
+using TSmem = FwdSmem<kTR, 2>;  // double-buffered hidden chunk
 
 // Column sums over the tile's M rows: out[c * ostride] = sum_r a[r * lda + c] * b(r, c)
 // for the 128 embed columns, where b(r, c) is b[r * ldb + c] (ldb > 0), the
@@ -93,7 +94,7 @@ __device__ __forceinline__ void bwd_head(const float* Wh, const float* dheadL, i
 // tile's forward captures (LDS). The tile's sums for dgamma (xn * dZ) and
 // dbeta (dZ) go to tp_gamma / tp_beta (the reference adds them with float
 // atomics).
-__device__ __forceinline__ void bwd_layernorm(FwdSmem<kTR>& sm, TRegs& G, const float* xn, const float* sd,
+__device__ __forceinline__ void bwd_layernorm(TSmem& sm, TRegs& G, const float* xn, const float* sd,
                                               const float* gamma, float* tp_gamma, float* tp_beta, float* scratch) {
     constexpr int TPR = kTNT / kTR, CPT = kEmbed / TPR;
     const int tid = threadIdx.x;
@@ -144,14 +145,15 @@ struct BwdSeq {
 // gradient at the block input. Chunked like the forward: dV_c = (dh Down_c^T)
 // masked by relu, then dx += dV_c Up_c^T; both weight reads are contiguous
 // float4s along the contraction; ws streams the backward sequence (BwdSeq).
-__device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSmem<kTR>& sm, TRegs& D,
+__device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem& sm, TRegs& D,
                                           TStream& ws, const float* v_tile, float* dv_store, float* dh_store,
                                           const float* xn_tile, const float* sd_tile, const float* gamma,
                                           float* tp, float* scratch) {
     const int H = (int)pv.hidden, NC = H / kChunk;
     const BwdSeq seq{&pv, NC};
-    store_tile<kTR, kTW>(D.h, sm.xs, dh_store, kEmbed, 0);
+    store_tile<kTR, kTW>(D.h, sm.xs);
     __syncthreads();
+    copy_rows_g<kTR, kTNT>(sm.xs, dh_store, kEmbed);
     TRegs G;
     zero<kTR, kTW>(G.h);
     for (int c = 0; c < NC; ++c) {
@@ -162,17 +164,16 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSm
         for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
             mask[rt][ct][r] = v_tile[(size_t)row * H + kChunk * c + col];
         });
+        float* vs = sm.vs[c & 1];  // double-buffered: no barrier before the write
         TS::Acc v[TS::RT][TS::CT];
         zero<kTR, kTW>(v);
         ws.template gemm<0>(v, sm.xs, s, seq);
-        __syncthreads();
         for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-            const float x = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
-            sm.vs[row * kLds + col] = x;
-            dv_store[(size_t)row * H + kChunk * c + col] = x;
+            vs[row * kLds + col] = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
         });
         __syncthreads();
-        ws.template gemm<1>(G.h, sm.vs, s + 1, seq);
+        copy_rows_g<kTR, kTNT>(vs, dv_store + kChunk * c, H);
+        ws.template gemm<1>(G.h, vs, s + 1, seq);
     }
     __syncthreads();
     bwd_layernorm(sm, G, xn_tile, sd_tile, gamma, tp + pv.off_ln_gamma[l], tp + pv.off_ln_beta[l], scratch);
@@ -185,7 +186,7 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, FwdSm
 // LDS of one train_rows workgroup. The LN captures xn / sd are only read by
 // the LN backward, so they never leave the CU.
 struct RowsSmem {
-    FwdSmem<kTR> sm;
+    TSmem sm;
     float xn[(MG_MAX_LAYERS + 1) * kTR * kEmbed];
     float sd[(MG_MAX_LAYERS + 1) * kTR];
     float ln[(MG_MAX_LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
@@ -201,7 +202,7 @@ struct RowsSmem {
 __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     constexpr int M = kTR;
     __shared__ RowsSmem L;
-    FwdSmem<M>& sm = L.sm;
+    TSmem& sm = L.sm;
     TRegs R;
     const mg_policy_view& pv = a.pv;
     const TrainWs& ws = a.ws;
@@ -241,7 +242,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     for (int l = 0; l < NL; ++l) {
         fwd_layernorm<M, kTW>(sm, R, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, L.xn + l * M * kEmbed,
                               L.sd + l * M, ws.x + ((size_t)l * B + r0) * kEmbed);
-        fwd_block<M, kTW>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H);
+        fwd_block<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H);
     }
     // the backward's first weights are in flight through the final LN, the head and the loss
     wst.start(2 * NL * (H / kChunk), BwdSeq{&pv, H / kChunk});
