@@ -336,15 +336,16 @@ struct FwdSeq {
 // One residual block (model/mlp.metal:18-86 + model/elementwise.metal:4-13):
 // h += relu(xs Up) Down, the hidden dimension in 128-wide chunks whose Down
 // products accumulate straight into the residual stream (the residual add
-// folded into the GEMM accumulator). xs holds LN(h); ws streams the forward
-// sequence (FwdSeq). With VOUT the relu'd hidden activations are also written
-// to v_out ([M][hidden], row-major).
-template <int M, int W = 4, bool VOUT = false, int NV = 1>
+// folded into the GEMM accumulator). xs holds LN(h); ws streams a sequence
+// whose first 2 L NC GEMMs are the forward's (FwdSeq, or a longer sequence
+// that continues past the forward). With VOUT the relu'd hidden activations
+// are also written to v_out ([M][hidden], row-major).
+template <int M, int W = 4, bool VOUT = false, int NV = 1, class Seq = FwdSeq>
 __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M, NV>& sm, FwdRegs<M, W>& R,
-                                          WStream<M, W>& ws, float* v_out = nullptr) {
+                                          WStream<M, W>& ws, float* v_out = nullptr, Seq seq = Seq{}) {
     using S = Shape<M, W>;
     const int H = (int)pv.hidden, NC = H / kChunk;
-    const FwdSeq seq{&pv, NC};
+    if constexpr (std::is_same<Seq, FwdSeq>::value) seq = FwdSeq{&pv, NC};
     for (int c = 0; c < NC; ++c) {
         const int s = 2 * (l * NC + c);
         float* vs = sm.vs[NV == 2 ? (c & 1) : 0];

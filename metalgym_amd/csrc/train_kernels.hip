@@ -140,24 +140,36 @@ struct BwdSeq {
     }
 };
 
+// The row pass streams one sequence: the forward's 2 L NC GEMMs, then the
+// backward's, so the last forward GEMMs already prefetch the backward's first
+// weights.
+struct TrainSeq {
+    const mg_policy_view* pv;
+    int nc;
+    __device__ __forceinline__ FragSrc operator()(int s) const {
+        const int F = 2 * (int)pv->layers * nc;
+        return s < F ? FwdSeq{pv, nc}(s) : BwdSeq{pv, nc}(s - F);
+    }
+};
+
 // Backward of block l (model/mlp.metal:88-153 + model/ppo.h:851-852). D holds
 // the gradient at the block output (dStream) and is updated in place to the
 // gradient at the block input. Chunked like the forward: dV_c = (dh Down_c^T)
 // masked by relu, then dx += dV_c Up_c^T; both weight reads are contiguous
-// float4s along the contraction; ws streams the backward sequence (BwdSeq).
+// float4s along the contraction; ws streams the row pass's TrainSeq.
 __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem& sm, TRegs& D,
                                           TStream& ws, const float* v_tile, float* dv_store, float* dh_store,
                                           const float* xn_tile, const float* sd_tile, const float* gamma,
                                           float* tp, float* scratch) {
-    const int H = (int)pv.hidden, NC = H / kChunk;
-    const BwdSeq seq{&pv, NC};
+    const int H = (int)pv.hidden, NC = H / kChunk, F = 2 * (int)pv.layers * NC;
+    const TrainSeq seq{&pv, NC};
     store_tile<kTR, kTW>(D.h, sm.xs);
     __syncthreads();
     copy_rows_g<kTR, kTNT>(sm.xs, dh_store, kEmbed);
     TRegs G;
     zero<kTR, kTW>(G.h);
     for (int c = 0; c < NC; ++c) {
-        const int s = 2 * (((int)pv.layers - 1 - l) * NC + c);
+        const int s = F + 2 * (((int)pv.layers - 1 - l) * NC + c);
         // the relu mask of this chunk, loaded before the GEMM issues its weight
         // refills (vector memory counters complete in order)
         TS::Acc mask[TS::RT][TS::CT];
@@ -234,7 +246,8 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
         if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
     }
     TStream wst;
-    fwd_start<M, kTW>(pv, wst);
+    const TrainSeq seq{&pv, H / kChunk};
+    wst.start(4 * NL * (H / kChunk), seq);
     __syncthreads();
 
     // ---- forward with capture ----
@@ -242,10 +255,9 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     for (int l = 0; l < NL; ++l) {
         fwd_layernorm<M, kTW>(sm, R, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, L.xn + l * M * kEmbed,
                               L.sd + l * M, ws.x + ((size_t)l * B + r0) * kEmbed);
-        fwd_block<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H);
+        fwd_block<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H, seq);
     }
     // the backward's first weights are in flight through the final LN, the head and the loss
-    wst.start(2 * NL * (H / kChunk), BwdSeq{&pv, H / kChunk});
     fwd_layernorm<M, kTW>(sm, R, L.ln + NL * 2 * kEmbed, L.ln + NL * 2 * kEmbed + kEmbed, L.xn + NL * M * kEmbed,
                           L.sd + NL * M, ws.x + ((size_t)NL * B + r0) * kEmbed);
     fwd_head<M, kTW>(L.wh, sm, L.head, HD);
