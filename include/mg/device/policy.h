@@ -156,6 +156,44 @@ __device__ __forceinline__ void gemm_frag(AccTile<M, W>& acc, const float* a_lds
                 for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[g][rt][j], f.b[g][ct][j], acc[rt][ct]);
 }
 
+// gemm_frag fused with the refill of the same registers: k-group g's weights
+// are replaced by k-group g of `next` as soon as its MFMAs have issued, so a
+// wave's refill loads leave one at a time over the GEMM instead of as a burst
+// after it (a burst from every wave of the CU backs up the CU's vector-memory
+// address path and stalls the issuing waves).
+template <int M, int W, int NG>
+__device__ __forceinline__ void gemm_frag_refill(AccTile<M, W>& acc, const float* a_lds, BFrag<M, W, NG>& f,
+                                                 const float* next_p, size_t next_ld, int g0) {
+    using S = Shape<M, W>;
+    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane), n0 = S::SW * (threadIdx.x >> 6);
+    const float* ap = a_lds + n * kLds + 4 * q + S::KG * g0;
+    const float* bp = next_p + (size_t)(n0 + n) * next_ld + 4 * q + S::KG * g0;
+    f32x4 a[NG][S::RT];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int rt = 0; rt < S::RT; ++rt)
+            a[g][rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[g][rt][j], f.b[g][ct][j], acc[rt][ct]);
+#pragma unroll
+        for (int ct = 0; ct < S::CT; ++ct) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(bp + (size_t)(S::MT * ct) * next_ld + S::KG * g);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
+        }
+        // keep the interleave: the scheduler would otherwise sink every load
+        // to the end of the GEMM to shorten their live ranges
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Where the s-th weight operand of a GEMM sequence lives (transposed layout).
 struct FragSrc {
     const float* p;
@@ -204,8 +242,7 @@ struct WStream {
     __device__ __forceinline__ void gemm(AccTile<M, W>& acc, const float* a_lds, int s, Src src) {
         if constexpr (WHOLE) {
             const FragSrc f = src(s + 2 < total ? s + 2 : s);
-            gemm_frag<M, W, NG>(acc, a_lds, b[ROLE], 0);
-            load_frag_t<M, W, NG>(b[ROLE], f.p, f.ld, 0);
+            gemm_frag_refill<M, W, NG>(acc, a_lds, b[ROLE], f.p, f.ld, 0);
         } else {
             const bool more = s + 1 < total;
             FragSrc f{nullptr, 0};

@@ -5,21 +5,25 @@
 // threshold flips a done flag, and a flipped done flag changes how many reset
 // draws an env takes from its RNG stream. libm and the device libraries do not
 // promise identical results, so every transcendental used by per-env code is
-// computed here from IEEE double arithmetic only (+, -, *, / and exact bit
-// manipulation), then rounded once to float. IEEE double operations are
-// correctly rounded on x86-64 SSE2 and on CDNA, so both sides agree bit for bit
-// as long as floating-point contraction is off (every build of this project
-// passes -ffp-contract=off).
+// computed here from IEEE float arithmetic only (+, -, *, / and exact bit
+// manipulation), in one fixed order. IEEE float operations are correctly
+// rounded on x86-64 SSE and on CDNA, so both sides agree bit for bit as long as
+// floating-point contraction is off (every build of this project passes
+// -ffp-contract=off). Tested against correctly rounded values: expf, sinf and
+// cosf within 1 ulp, logf within 2, tanhf within 3. sin/cos arguments with
+// |x| >= 8 take an exact double-precision path, identically on both sides.
 //
 // Methods (all textbook, named per function):
-//   expf   : argument reduction x = k ln2 + r (Cody & Waite 1980, two-part ln2),
-//            Taylor series of e^r to degree 13, scaled by 2^k.
-//   expm1  : Taylor series for |y| < 0.5, else exp - 1.
+//   expf   : x = k ln2 + r (Cody & Waite 1980, two-part ln2 whose high part
+//            has 9 significant bits, so k * high is exact), Taylor series of
+//            e^r to degree 7, scaled by 2^k through the exponent bits.
 //   logf   : x = 2^e m, m in [sqrt(1/2), sqrt(2)); log m = 2 atanh(s),
-//            s = (m-1)/(m+1), odd series to s^21 (Abramowitz & Stegun 4.1.27).
-//   sinf/cosf : reduction by pi/2 with a three-part pi/2 (Cody & Waite), Taylor
-//            series on [-pi/4, pi/4] to degree 17/18, quadrant selection.
-//   tanhf  : tanh x = expm1(2x) / (expm1(2x) + 2).
+//            s = (m-1)/(m+1), odd series to s^9 (Abramowitz & Stegun 4.1.27).
+//   sincosf: reduction by pi/2 with a three-part pi/2 (Cody & Waite), Taylor
+//            series on [-pi/4, pi/4] to degree 9 (sin) and 10 (cos),
+//            quadrant selection; |x| <= pi/4 skips the reduction.
+//   tanhf  : tanh |x| = expm1(2|x|) / (expm1(2|x|) + 2), expm1 by its Taylor
+//            series below 0.5, else e^y - 1.
 #pragma once
 #include <stdint.h>
 
@@ -85,19 +89,6 @@ MG_HD double exp_d(double x) {
     return exp_taylor_d(r) * pow2_d(k);
 }
 
-MG_HD float expf(float x) {
-    if (x != x) return x;
-    if (x > 88.7228394f) return bits_to_float(0x7f800000u);
-    if (x < -103.972084f) return 0.0f;
-    double xd = (double)x;
-    int k = round_to_int(xd * kInvLn2);
-    double r = (xd - (double)k * kLn2Hi) - (double)k * kLn2Lo;
-    double p = exp_taylor_d(r);
-    // split the scale so each factor stays a normal double
-    int k1 = k / 2;
-    return (float)(p * pow2_d(k1) * pow2_d(k - k1));
-}
-
 // e^y - 1 in double.
 MG_HD double expm1_d(double y) {
     if (y > -0.5 && y < 0.5) {
@@ -123,49 +114,6 @@ MG_HD double expm1_d(double y) {
         return p * y;
     }
     return exp_d(y) - 1.0;
-}
-
-MG_HD float tanhf(float x) {
-    if (x != x) return x;
-    if (x > 10.0f) return 1.0f;
-    if (x < -10.0f) return -1.0f;
-    double e = expm1_d(2.0 * (double)x);
-    return (float)(e / (e + 2.0));
-}
-
-MG_HD float logf(float x) {
-    uint32_t b = float_to_bits(x);
-    if (x != x) return x;
-    if (x < 0.0f) return bits_to_float(0x7fc00000u);
-    if (x == 0.0f) return bits_to_float(0xff800000u);
-    if (b == 0x7f800000u) return x;
-    int e = 0;
-    if ((b >> 23) == 0) {  // subnormal: scale by 2^25
-        x = x * 33554432.0f;
-        b = float_to_bits(x);
-        e = -25;
-    }
-    e += (int)(b >> 23) - 127;
-    double m = (double)bits_to_float((b & 0x007fffffu) | 0x3f800000u);  // [1, 2)
-    if (m > 1.41421356237309504880) {
-        m = m * 0.5;
-        e += 1;
-    }
-    double s = (m - 1.0) / (m + 1.0);
-    double s2 = s * s;
-    double p = 1.0 / 21.0;
-    p = p * s2 + 1.0 / 19.0;
-    p = p * s2 + 1.0 / 17.0;
-    p = p * s2 + 1.0 / 15.0;
-    p = p * s2 + 1.0 / 13.0;
-    p = p * s2 + 1.0 / 11.0;
-    p = p * s2 + 1.0 / 9.0;
-    p = p * s2 + 1.0 / 7.0;
-    p = p * s2 + 1.0 / 5.0;
-    p = p * s2 + 1.0 / 3.0;
-    p = p * s2 + 1.0;
-    double lm = 2.0 * s * p;
-    return (float)((double)e * kLn2 + lm);
 }
 
 constexpr double kTwoOverPi = 6.36619772367581382433e-01;
@@ -211,34 +159,179 @@ MG_HD double reduce_pio2(float x, int* q) {
     return r;
 }
 
-MG_HD float sinf(float x) {
+// ---- float paths ------------------------------------------------------------
+
+// 2^k as a float for k in [-126, 127], exact.
+MG_HD float pow2_f(int k) { return bits_to_float((uint32_t)(k + 127) << 23); }
+
+// Round to nearest integer (ties away from zero) for |x| < 2^22.
+MG_HD int round_to_int_f(float x) { return x >= 0.0f ? (int)(x + 0.5f) : -(int)(-x + 0.5f); }
+
+constexpr float kLn2HiF = 0.693359375f;         // 355/512: k * kLn2HiF is exact for |k| < 2^15
+constexpr float kLn2LoF = -2.12194440e-4f;      // ln2 - kLn2HiF
+constexpr float kInvLn2F = 1.44269502162933349609f;
+constexpr float kLn2F = 0.693147182464599609375f;
+
+// e^r for |r| <= 0.35 by Taylor series (Horner), degree 7.
+MG_HD float exp_taylor_f(float r) {
+    float p = 1.0f / 5040.0f;
+    p = p * r + 1.0f / 720.0f;
+    p = p * r + 1.0f / 120.0f;
+    p = p * r + 1.0f / 24.0f;
+    p = p * r + 1.0f / 6.0f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return p;
+}
+
+// e^x. Arguments below -87 return 0, so every nonzero result is a normal
+// float (no dependence on either side's subnormal handling).
+MG_HD float expf(float x) {
     if (x != x) return x;
-    if (float_to_bits(x) << 1 == 0xff000000u) return bits_to_float(0x7fc00000u);  // +-inf
-    int q;
-    double r = reduce_pio2(x, &q);
-    double v;
-    switch (q) {
-        case 0: v = sin_taylor_d(r); break;
-        case 1: v = cos_taylor_d(r); break;
-        case 2: v = -sin_taylor_d(r); break;
-        default: v = -cos_taylor_d(r); break;
+    if (x > 88.7228394f) return bits_to_float(0x7f800000u);
+    if (x < -87.0f) return 0.0f;
+    const int k = round_to_int_f(x * kInvLn2F);
+    const float kf = (float)k;
+    const float r = (x - kf * kLn2HiF) - kf * kLn2LoF;
+    const float p = exp_taylor_f(r);
+    // two factors so each stays a normal float at the ends of the range
+    const int k1 = k / 2;
+    return (p * pow2_f(k1)) * pow2_f(k - k1);
+}
+
+// e^y - 1 for y >= 0.
+MG_HD float expm1_pos_f(float y) {
+    if (y < 0.5f) {
+        float p = 1.0f / 40320.0f;  // 1/8!
+        p = p * y + 1.0f / 5040.0f;
+        p = p * y + 1.0f / 720.0f;
+        p = p * y + 1.0f / 120.0f;
+        p = p * y + 1.0f / 24.0f;
+        p = p * y + 1.0f / 6.0f;
+        p = p * y + 0.5f;
+        p = p * y + 1.0f;
+        return p * y;
     }
-    return (float)v;
+    return expf(y) - 1.0f;
+}
+
+MG_HD float tanhf(float x) {
+    if (x != x) return x;
+    const float ax = x < 0.0f ? -x : x;
+    if (ax > 9.0f) return x < 0.0f ? -1.0f : 1.0f;
+    const float e = expm1_pos_f(2.0f * ax);
+    const float t = e / (e + 2.0f);
+    return x < 0.0f ? -t : t;
+}
+
+MG_HD float logf(float x) {
+    uint32_t b = float_to_bits(x);
+    if (x != x) return x;
+    if (x < 0.0f) return bits_to_float(0x7fc00000u);
+    if (x == 0.0f) return bits_to_float(0xff800000u);
+    if (b == 0x7f800000u) return x;
+    int e = 0;
+    if ((b >> 23) == 0) {  // subnormal: scale by 2^25
+        x = x * 33554432.0f;
+        b = float_to_bits(x);
+        e = -25;
+    }
+    e += (int)(b >> 23) - 127;
+    float m = bits_to_float((b & 0x007fffffu) | 0x3f800000u);  // [1, 2)
+    if (m > 1.41421356f) {
+        m = m * 0.5f;
+        e += 1;
+    }
+    const float s = (m - 1.0f) / (m + 1.0f);
+    const float s2 = s * s;
+    float p = 1.0f / 9.0f;
+    p = p * s2 + 1.0f / 7.0f;
+    p = p * s2 + 1.0f / 5.0f;
+    p = p * s2 + 1.0f / 3.0f;
+    const float ef = (float)e;
+    // log x = e ln2 + 2 s + 2 s^3 p, small terms first
+    const float lm = 2.0f * s + (2.0f * s) * s2 * p;
+    return ef * kLn2HiF + (ef * kLn2LoF + lm);
+}
+
+MG_HD float sin_taylor_f(float r) {  // |r| <= pi/4, degree 9
+    const float r2 = r * r;
+    float q = 1.0f / 362880.0f;
+    q = q * r2 - 1.0f / 5040.0f;
+    q = q * r2 + 1.0f / 120.0f;
+    q = q * r2 - 1.0f / 6.0f;
+    return r + r * r2 * q;
+}
+
+MG_HD float cos_taylor_f(float r) {  // |r| <= pi/4, degree 10
+    const float r2 = r * r;
+    float q = -1.0f / 3628800.0f;
+    q = q * r2 + 1.0f / 40320.0f;
+    q = q * r2 - 1.0f / 720.0f;
+    q = q * r2 + 1.0f / 24.0f;
+    q = q * r2 - 0.5f;
+    return 1.0f + r2 * q;
+}
+
+constexpr float kPio4F = 0.785398163f;
+constexpr float kTwoOverPiF = 0.636619746685028076171875f;
+// pi/2 = kPio2_1F + kPio2_2F + kPio2_3F: the first two have 8 and 12
+// significant bits (k times either is exact for the |k| <= 5 of the float
+// path), the third is the float nearest the remainder.
+constexpr float kPio2_1F = 1.5703125f;
+constexpr float kPio2_2F = 4.83870506286621093750e-4f;
+constexpr float kPio2_3F = -4.37113883e-8f;
+
+// sin and cos of x with one shared reduction.
+MG_HD void sincosf(float x, float* s, float* c) {
+    if (x != x || float_to_bits(x) << 1 == 0xff000000u) {  // NaN, +-inf
+        *s = *c = bits_to_float(0x7fc00000u);
+        return;
+    }
+    const float ax = x < 0.0f ? -x : x;
+    if (ax <= kPio4F) {
+        *s = sin_taylor_f(x);
+        *c = cos_taylor_f(x);
+        return;
+    }
+    float r;
+    int q;
+    if (ax < 8.0f) {
+        const int k = round_to_int_f(x * kTwoOverPiF);
+        const float kf = (float)k;
+        r = ((x - kf * kPio2_1F) - kf * kPio2_2F) - kf * kPio2_3F;
+        q = k & 3;
+        const float sr = sin_taylor_f(r), cr = cos_taylor_f(r);
+        switch (q) {
+            case 0: *s = sr, *c = cr; break;
+            case 1: *s = cr, *c = -sr; break;
+            case 2: *s = -sr, *c = -cr; break;
+            default: *s = -cr, *c = sr; break;
+        }
+        return;
+    }
+    // large arguments: the exact double-precision path
+    const double rd = reduce_pio2(x, &q);
+    const double sd = sin_taylor_d(rd), cd = cos_taylor_d(rd);
+    switch (q) {
+        case 0: *s = (float)sd, *c = (float)cd; break;
+        case 1: *s = (float)cd, *c = (float)-sd; break;
+        case 2: *s = (float)-sd, *c = (float)-cd; break;
+        default: *s = (float)-cd, *c = (float)sd; break;
+    }
+}
+
+MG_HD float sinf(float x) {
+    float s, c;
+    sincosf(x, &s, &c);
+    return s;
 }
 
 MG_HD float cosf(float x) {
-    if (x != x) return x;
-    if (float_to_bits(x) << 1 == 0xff000000u) return bits_to_float(0x7fc00000u);
-    int q;
-    double r = reduce_pio2(x, &q);
-    double v;
-    switch (q) {
-        case 0: v = cos_taylor_d(r); break;
-        case 1: v = -sin_taylor_d(r); break;
-        case 2: v = -cos_taylor_d(r); break;
-        default: v = sin_taylor_d(r); break;
-    }
-    return (float)v;
+    float s, c;
+    sincosf(x, &s, &c);
+    return c;
 }
 
 }  // namespace mg
