@@ -264,9 +264,12 @@ def main():
         extra["full_ppo_262144"] = bench_full("rollout_cartpole", 262144, 32, 1, O, A)
         _, _, dtc, _ = bench_collect("rollout_cartpole_continuous", 262144, 32, 3, 1, 4, 1)
         extra["continuous_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtc}
+        extra["continuous_full_ppo_65536"] = bench_full("rollout_cartpole_continuous", 65536, 32, 2, 4, 1)
+        extra["continuous_full_ppo_262144"] = bench_full("rollout_cartpole_continuous", 262144, 32, 1, 4, 1)
         _, _, dtv, tv = bench_collect("rollout_voxelnav16", 262144, 32, 3, 1, 30, 6)
         extra["voxelnav16_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtv,
                                               "collect_ms": kernel_avg_ms(tv, "collect")}
+        extra["voxelnav16_full_ppo_262144"] = bench_full("rollout_voxelnav16", 262144, 32, 1, 30, 6)
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

@@ -37,31 +37,39 @@ using TRegs = FwdRegs<kTR, kTW>;
 using TStream = WStream<kTR, kTW>;
 using TSmem = FwdSmem<kTR, 2>;  // double-buffered hidden chunk
 
-// Column sums over the tile's M rows: out[c * ostride] = sum_r a[r * lda + c] * b(r, c)
-// for the 128 embed columns, where b(r, c) is b[r * ldb + c] (ldb > 0), the
-// per-row scalar b[r * bstride] (ldb == 0), or 1 (b == nullptr). The workgroup's
-// NT / 128 thread groups each sum a range of rows; the ranges are added in
-// order. `scratch` is NT floats of LDS; ends with a barrier.
+// Per-tile outer-product sums in one pass: out[k * ks + c * cs] =
+// sum_r a[r * lda + k] * b[r * kLds + c] for k < K and the 128 columns c, rows
+// added in order by one thread per output. a and b are LDS tiles of M rows.
+// No barrier (the caller orders the inputs before and the outputs after).
 template <int M, int NT>
-__device__ __forceinline__ void tile_colsum(const float* a, int lda, const float* b, int ldb, int bstride,
-                                            float* out, int ostride, float* scratch) {
-    constexpr int P = NT / kEmbed, RP = M / P;
-    const int t = threadIdx.x, c = t & (kEmbed - 1), part = t / kEmbed;
-    float s = 0.0f;
+__device__ __forceinline__ void tile_outer(const float* a, int lda, int K, const float* b, float* out, int ks,
+                                           int cs) {
+    for (int idx = threadIdx.x; idx < K * kEmbed; idx += NT) {
+        const int k = idx / kEmbed, c = idx % kEmbed;
+        float s = 0.0f;
 #pragma unroll
-    for (int r = part * RP; r < (part + 1) * RP; ++r) {
-        const float x = a[r * lda + c];
-        s += b ? x * (ldb ? b[r * ldb + c] : b[r * bstride]) : x;
+        for (int r = 0; r < M; ++r) s += a[r * lda + k] * b[r * kLds + c];
+        out[k * ks + c * cs] = s;
     }
-    scratch[t] = s;
-    __syncthreads();
-    if (t < kEmbed) {
-        float o = scratch[c];
+}
+
+// Column sums of an LDS tile of M rows (sum_r b[r * kLds + c]) and, if a is
+// given, of its products with another tile (sum_r a[r * kEmbed + c] b[...]),
+// rows in order; threads 0..127 one column each. No barrier.
+template <int M>
+__device__ __forceinline__ void tile_colsum2(const float* b, const float* a, float* out_sum, float* out_prod) {
+    const int c = threadIdx.x;
+    if (c < kEmbed) {
+        float s = 0.0f, p = 0.0f;
 #pragma unroll
-        for (int p = 1; p < P; ++p) o += scratch[p * kEmbed + c];
-        out[c * ostride] = o;
+        for (int r = 0; r < M; ++r) {
+            const float x = b[r * kLds + c];
+            s += x;
+            if (a) p += a[r * kEmbed + c] * x;
+        }
+        out_sum[c] = s;
+        if (a) out_prod[c] = p;
     }
-    __syncthreads();
 }
 
 struct RowsArgs {
@@ -100,8 +108,8 @@ __device__ __forceinline__ void bwd_layernorm(TSmem& sm, TRegs& G, const float* 
     const int tid = threadIdx.x;
     store_tile<kTR, kTW>(G.h, sm.xs);
     __syncthreads();
-    tile_colsum<kTR, kTNT>(sm.xs, kLds, xn, kEmbed, 0, tp_gamma, 1, scratch);
-    tile_colsum<kTR, kTNT>(sm.xs, kLds, nullptr, 0, 0, tp_beta, 1, scratch);
+    tile_colsum2<kTR>(sm.xs, xn, tp_beta, tp_gamma);  // reads the tile before the in-place update below
+    __syncthreads();
     const int row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     float* zr = sm.xs + row * kLds + c0;
     const float* xr = xn + row * kEmbed + c0;
@@ -332,8 +340,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
 
     // model/linear.metal:71-93 on this tile: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
     // (sm.xs still holds the final LN output x_f)
-    for (int j = 0; j < HD; ++j)
-        tile_colsum<M, kTNT>(sm.xs, kLds, L.dhead + j, 0, HD, tp + pv.float_group + j, HD, L.scratch);
+    tile_outer<M, kTNT>(L.dhead, HD, HD, sm.xs, tp + pv.float_group, 1, HD);
     if (pv.continuous && tid < A) {  // model/gaussian.metal:166-168, summed over the tile in row order
         float s = 0.0f;
         for (int r = 0; r < M; ++r) s += L.dls[r * A + tid];
@@ -345,6 +352,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
         for (int r = 0; r < M; ++r) s += L.stat[r * 5 + q];
         tp[pv.float_group + kEmbed * HD + q] = s;
     }
+    __syncthreads();  // every read of x_f in sm.xs is done before the LN backward overwrites it
 
     // ---- backward ----
     TRegs D;
@@ -359,9 +367,8 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     // model/input.metal:38-60 on this tile: dW_in[k][c] = sum_r obs[r][k] dh0[r][c], db_in = sum_r dh0
     store_tile<M, kTW>(D.h, sm.xs);
     __syncthreads();
-    tile_colsum<M, kTNT>(sm.xs, kLds, nullptr, 0, 0, tp + pv.off_in_b, 1, L.scratch);
-    for (int k = 0; k < O; ++k)
-        tile_colsum<M, kTNT>(sm.xs, kLds, L.obs + k, 0, O, tp + pv.off_in_w + k * kEmbed, 1, L.scratch);
+    tile_colsum2<M>(sm.xs, nullptr, tp + pv.off_in_b, nullptr);
+    tile_outer<M, kTNT>(L.obs, O, O, sm.xs, tp + pv.off_in_w, kEmbed, 1);
 }
 
 // ---- weight gradients ---------------------------------------------------------
