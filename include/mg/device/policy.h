@@ -255,6 +255,88 @@ struct WStream {
     }
 };
 
+// Weight stream for 16-row tiles that stages each GEMM's weights through a
+// private LDS scratch of the wave. The MFMA operand layout puts 16 different
+// weight rows (64 B each) in one float4 load, 16 L1 requests per KB; here each
+// load instruction covers two whole 512-byte rows (8 cache lines per KB), the
+// rows go to the wave's scratch XOR-swizzled (slot r * 32 + (c ^ (r & 7)) for
+// row r, 16-byte chunk c), and the GEMM reads them back in MFMA layout without
+// bank conflicts. Only the owning wave touches its scratch, so no barrier is
+// needed: a wave's LDS operations complete in order. Each GEMM writes its
+// weights to the scratch first, then issues the loads of the GEMM two ahead,
+// one per k-group between the MFMAs. (Writing the next GEMM's weights in the
+// middle of this one measured slower: that write waits for loads issued only
+// one GEMM earlier and stalls the MFMAs behind it.) Same interface as WStream.
+template <int M, int W>
+struct LStream {
+    using S = Shape<M, W>;
+    static_assert(S::MT == 16 && S::SW % 2 == 0, "16x16x4 tiles, two rows per load");
+    static constexpr int NI = S::SW / 2;        // raw float4 loads per lane per GEMM
+    static constexpr int NGF = kEmbed / S::KG;  // k-groups of one 128-deep GEMM
+    static_assert(NI <= NGF, "one refill load per k-group at most");
+    f32x4 raw[2][NI];
+    float* scr;  // this wave's scratch: SW rows x 128 floats
+    int total;
+
+    __device__ __forceinline__ void load_raw(int role, const FragSrc& f, int i) {
+        const int lane = threadIdx.x & 63, n0 = S::SW * (threadIdx.x >> 6);
+        raw[role][i] = *reinterpret_cast<const f32x4*>(f.p + (size_t)(n0 + 2 * i + (lane >> 5)) * f.ld +
+                                                       4 * (lane & 31));
+    }
+    static __device__ __forceinline__ int slot(int r, int c) { return r * 32 + (c ^ (r & 7)); }
+    __device__ __forceinline__ void write_scratch(int role) {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int r = 2 * i + (lane >> 5);
+            *reinterpret_cast<f32x4*>(scr + 4 * slot(r, lane & 31)) = raw[role][i];
+        }
+    }
+
+    // n >= 2 GEMMs; scratch = SW * 128 floats of LDS owned by this wave.
+    template <class Src>
+    __device__ __forceinline__ void start(int n, Src src, float* scratch) {
+        total = n;
+        scr = scratch;
+        const FragSrc f0 = src(0), f1 = src(1);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) load_raw(0, f0, i);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) load_raw(1, f1, i);
+    }
+
+    template <int ROLE, class Src>
+    __device__ __forceinline__ void gemm(AccTile<M, W>& acc, const float* a_lds, int s, Src src) {
+        const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
+        write_scratch(ROLE);
+        const FragSrc f = src(s + 2 < total ? s + 2 : s);
+        const float* ap = a_lds + n * kLds + 4 * q;
+        f32x4 a[NGF][S::RT];
+#pragma unroll
+        for (int g = 0; g < NGF; ++g)
+#pragma unroll
+            for (int rt = 0; rt < S::RT; ++rt)
+                a[g][rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
+        f32x4 b[NGF][S::CT];
+#pragma unroll
+        for (int g = 0; g < NGF; ++g)
+#pragma unroll
+            for (int ct = 0; ct < S::CT; ++ct)
+                b[g][ct] = *reinterpret_cast<const f32x4*>(scr + 4 * slot(n + S::MT * ct, 4 * g + q));
+#pragma unroll
+        for (int g = 0; g < NGF; ++g) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+                    for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[g][rt][j], b[g][ct][j], acc[rt][ct]);
+            if (g < NI) load_raw(ROLE, f, g);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
 // Writes a register tile to LDS (row stride kLds), optionally through relu.
 template <int M, int W = 4, bool RELU = false>
 __device__ __forceinline__ void store_tile(const AccTile<M, W>& acc, float* lds) {
@@ -377,9 +459,9 @@ struct FwdSeq {
 // whose first 2 L NC GEMMs are the forward's (FwdSeq, or a longer sequence
 // that continues past the forward). With VOUT the relu'd hidden activations
 // are also written to v_out ([M][hidden], row-major).
-template <int M, int W = 4, bool VOUT = false, int NV = 1, class Seq = FwdSeq>
+template <int M, int W = 4, bool VOUT = false, int NV = 1, class Seq = FwdSeq, class Stream = WStream<M, W>>
 __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M, NV>& sm, FwdRegs<M, W>& R,
-                                          WStream<M, W>& ws, float* v_out = nullptr, Seq seq = Seq{}) {
+                                          Stream& ws, float* v_out = nullptr, Seq seq = Seq{}) {
     using S = Shape<M, W>;
     const int H = (int)pv.hidden, NC = H / kChunk;
     if constexpr (std::is_same<Seq, FwdSeq>::value) seq = FwdSeq{&pv, NC};

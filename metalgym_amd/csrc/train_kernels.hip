@@ -34,7 +34,6 @@ constexpr int kMaxHeadT = 64;
 constexpr int kMaxObsT = 64;
 using TS = Shape<kTR, kTW>;
 using TRegs = FwdRegs<kTR, kTW>;
-using TStream = WStream<kTR, kTW>;
 using TSmem = FwdSmem<kTR, 2>;  // double-buffered hidden chunk
 
 // Per-tile outer-product sums in one pass: out[k * ks + c * cs] =
@@ -165,8 +164,9 @@ struct TrainSeq {
 // gradient at the block input. Chunked like the forward: dV_c = (dh Down_c^T)
 // masked by relu, then dx += dV_c Up_c^T; both weight reads are contiguous
 // float4s along the contraction; ws streams the row pass's TrainSeq.
+template <class Stream>
 __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem& sm, TRegs& D,
-                                          TStream& ws, const float* v_tile, float* dv_store, float* dh_store,
+                                          Stream& ws, const float* v_tile, float* dv_store, float* dh_store,
                                           const float* xn_tile, const float* sd_tile, const float* gamma,
                                           float* tp, float* scratch) {
     const int H = (int)pv.hidden, NC = H / kChunk, F = 2 * (int)pv.layers * NC;
@@ -203,25 +203,42 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem
         for (int ct = 0; ct < TS::CT; ++ct) D.h[rt][ct] = G.h[rt][ct] + D.h[rt][ct];  // residualAdd(dBranch, dStream)
 }
 
-// LDS of one train_rows workgroup. The LN captures xn / sd are only read by
-// the LN backward, so they never leave the CU.
-struct RowsSmem {
-    TSmem sm;
-    float xn[(MG_MAX_LAYERS + 1) * kTR * kEmbed];
-    float sd[(MG_MAX_LAYERS + 1) * kTR];
-    float ln[(MG_MAX_LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
-    float wh[kEmbed * kMaxHeadT];                // W_head
-    float obs[kTR * kMaxObsT];
-    float head[kTR * kMaxHeadT];
-    float dhead[kTR * kMaxHeadT];
-    float dls[kTR * kMaxHeadT];
-    float stat[kTR * 5];
-    float scratch[kTNT];
+// Size classes of the row pass. Staged: LDS-staged weights (LStream) for up to
+// 4 blocks, obs <= 32 and head <= 16 floats, which leaves room for the 64 KB of
+// per-wave weight scratch; Wide: any supported shape, weights streamed straight
+// into registers (WStream).
+struct RowsStaged {
+    static constexpr int LMAX = 4, OMAX = 32, HDMAX = 16;
+    static constexpr bool STAGE = true;
+};
+struct RowsWide {
+    static constexpr int LMAX = MG_MAX_LAYERS, OMAX = kMaxObsT, HDMAX = kMaxHeadT;
+    static constexpr bool STAGE = false;
 };
 
+// LDS of one train_rows workgroup. The LN captures xn / sd are only read by
+// the LN backward, so they never leave the CU.
+template <class Cfg>
+struct RowsSmem {
+    TSmem sm;
+    float xn[(Cfg::LMAX + 1) * kTR * kEmbed];
+    float sd[(Cfg::LMAX + 1) * kTR];
+    float ln[(Cfg::LMAX + 1) * 2 * kEmbed];  // gamma, beta of every LN
+    float wh[kEmbed * Cfg::HDMAX];           // W_head
+    float obs[kTR * Cfg::OMAX];
+    float head[kTR * Cfg::HDMAX];
+    float dhead[kTR * Cfg::HDMAX];
+    float dls[kTR * Cfg::HDMAX];
+    float stat[kTR * 5];
+    float scratch[kTNT];
+    float wscr[Cfg::STAGE ? kTNT / 64 * TS::SW * kEmbed : 1];  // per-wave weight scratch
+};
+
+template <class Cfg>
 __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     constexpr int M = kTR;
-    __shared__ RowsSmem L;
+    using Stream = typename std::conditional<Cfg::STAGE, LStream<kTR, kTW>, WStream<kTR, kTW>>::type;
+    __shared__ RowsSmem<Cfg> L;
     TSmem& sm = L.sm;
     TRegs R;
     const mg_policy_view& pv = a.pv;
@@ -253,9 +270,12 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
         ret = a.ret_slots[gr];
         if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
     }
-    TStream wst;
+    Stream wst;
     const TrainSeq seq{&pv, H / kChunk};
-    wst.start(4 * NL * (H / kChunk), seq);
+    if constexpr (Cfg::STAGE)
+        wst.start(4 * NL * (H / kChunk), seq, L.wscr + (tid >> 6) * TS::SW * kEmbed);
+    else
+        wst.start(4 * NL * (H / kChunk), seq);
     __syncthreads();
 
     // ---- forward with capture ----
@@ -744,7 +764,13 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         ra.logp_slots = logp_slots;
         ra.adv_stats = adv_stats;
         ra.head_out = head_out;
-        hipLaunchKernelGGL(dev::train_rows_kernel, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
+        if (L <= (uint32_t)dev::RowsStaged::LMAX && pv.obs_dim <= (uint32_t)dev::RowsStaged::OMAX &&
+            pv.head_dim <= (uint32_t)dev::RowsStaged::HDMAX)
+            hipLaunchKernelGGL(dev::train_rows_kernel<dev::RowsStaged>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st,
+                               ra);
+        else
+            hipLaunchKernelGGL(dev::train_rows_kernel<dev::RowsWide>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st,
+                               ra);
         MG_HIP(hipGetLastError(), "train rows launch");
     }
     {  // 2. block-matrix weight gradients
