@@ -79,15 +79,17 @@ def float64_moment(pv, params, rows, hp):
     return 0.1 * g * scale
 
 
-@pytest.mark.parametrize("env,n,T,B,block", [
-    ("cartpole", 4096, 2, 4096, 1),
-    ("cartpole", 2048, 2, 512, 5),
-    ("cartpole", 1280, 2, 320, 3),      # minibatch not a multiple of 128
-    ("cartpole_continuous", 2048, 2, 1024, 2),
-    ("voxelnav16", 1024, 2, 512, 1),
+@pytest.mark.parametrize("env,n,T,B,block,layers,scale", [
+    ("cartpole", 4096, 2, 4096, 1, 2, 4),
+    ("cartpole", 2048, 2, 512, 5, 2, 4),
+    ("cartpole", 1280, 2, 320, 3, 2, 4),      # minibatch not a multiple of 128
+    ("cartpole_continuous", 2048, 2, 1024, 2, 2, 4),
+    ("voxelnav16", 1024, 2, 512, 1, 2, 4),
+    ("cartpole", 1024, 2, 512, 2, 3, 2),      # hidden 256, three blocks
+    ("cartpole", 1024, 2, 512, 1, 5, 2),      # five blocks: the row pass's register-streamed size class
 ])
-def test_one_minibatch(mg, orc, env, n, T, B, block):
-    gym, model, d = setup(mg, orc, env, n, T, B)
+def test_one_minibatch(mg, orc, env, n, T, B, block, layers, scale):
+    gym, model, d = setup(mg, orc, env, n, T, B, layers=layers, scale=scale)
     s = model.download_slots()
     p0 = model.params()
     hp = orc.hparams()
