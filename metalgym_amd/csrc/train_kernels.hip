@@ -434,27 +434,39 @@ __global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
         const uint32_t tm = t / ntn, tn = t % ntn;
         const int w = tid >> 6, lane = tid & 63, nn = lane & 31, hh = lane >> 5;
         const int wm = 32 * (w >> 1), wn = 32 * (w & 1);  // this wave's 32x32 sub-tile
-        // staging: each thread moves two float4 of X and two of Y per 32-row slab
+        // staging: each thread moves two float4 of X and two of Y per 32-row slab;
+        // the next slab is loaded into registers before this slab's MFMAs and
+        // written to LDS after them, so its load latency hides behind the MFMAs
         const int srow = tid >> 4, scol = (tid & 15) * 4;  // rows 0..15 (+16), columns 0..60
         const float* xg = bm.x + (size_t)rb * bm.ldx + tm * 64 + scol;
         const float* yg = bm.y + (size_t)rb * bm.ldy + tn * 64 + scol;
-        auto load = [&](int buf, uint32_t r0) {
+        f32x4 px[2], py[2];
+        auto fetch = [&](uint32_t r0) {
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
                 const int rr = srow + 16 * h2;
-                *reinterpret_cast<float4*>(&xs[buf][rr * kDwLd + scol]) =
-                    *reinterpret_cast<const float4*>(xg + (size_t)(r0 + rr) * bm.ldx);
-                *reinterpret_cast<float4*>(&ys[buf][rr * kDwLd + scol]) =
-                    *reinterpret_cast<const float4*>(yg + (size_t)(r0 + rr) * bm.ldy);
+                px[h2] = *reinterpret_cast<const f32x4*>(xg + (size_t)(r0 + rr) * bm.ldx);
+                py[h2] = *reinterpret_cast<const f32x4*>(yg + (size_t)(r0 + rr) * bm.ldy);
+            }
+        };
+        auto put = [&](int buf) {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int rr = srow + 16 * h2;
+                *reinterpret_cast<f32x4*>(&xs[buf][rr * kDwLd + scol]) = px[h2];
+                *reinterpret_cast<f32x4*>(&ys[buf][rr * kDwLd + scol]) = py[h2];
             }
         };
         f32x16 acc = f32x16{};
         const uint32_t steps = rowsPer / kDwRows;
-        load(0, 0);
+        fetch(0);
+        put(0);
         __syncthreads();
         for (uint32_t s = 0; s < steps; ++s) {
             const int cur = s & 1;
-            if (s + 1 < steps) load(cur ^ 1, (s + 1) * kDwRows);
+            // every step loads (the last one reloads its own slab, unused), so the
+            // wait counts are the same on every iteration
+            fetch((s + 1 < steps ? s + 1 : s) * kDwRows);
             const float* xc = xs[cur];
             const float* yc = ys[cur];
 #pragma unroll
@@ -465,6 +477,7 @@ __global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
                     acc = mfma32x32x2(xc[k * kDwLd + wm + nn], yc[k * kDwLd + wn + nn], acc);
                 }
             }
+            put(cur ^ 1);  // buffer cur ^ 1 was last read before the previous barrier
             __syncthreads();
         }
 #pragma unroll
