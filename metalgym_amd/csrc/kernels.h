@@ -36,7 +36,7 @@ struct TrainWs {
 };
 constexpr int kSplits = 16;        // row splits of the block-matrix gradient sums
 constexpr int kTileRows = 16;      // rows per train_rows workgroup
-constexpr int kReduceBlocks = 256; // workgroups of the gradient reduction
+constexpr int kReduceBlocks = 1024; // workgroups of the gradient reduction
 
 struct TrainStep {
     uint32_t row0;       // first slot row of the minibatch (t * n + r0)

@@ -491,10 +491,11 @@ __global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
 
 // The full gradient from its two sources, summed in fixed order, plus one
 // partial squared norm per workgroup:
-//  - workgroups [0, small_wgs): 64 tile-partial columns each (vector
-//    parameters, the head, then the 5 LossStats sums), four row groups of
-//    tiles per column added in order;
+//  - workgroups [0, small_wgs): 16 tile-partial columns each (vector
+//    parameters, the head, then the 5 LossStats sums); 16 thread groups per
+//    column each add a range of tiles, and the ranges are added in order;
 //  - the rest: the block matrices, the sum of the row splits (grid-stride).
+constexpr int kRedCols = 16;  // tile-partial columns per small workgroup
 struct ReduceArgs {
     const float* partial;
     const float* tp;
@@ -507,31 +508,35 @@ struct ReduceArgs {
 };
 
 __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
-    __shared__ float part[4][64];
+    constexpr int NG = 256 / kRedCols;  // thread groups per column
+    __shared__ float part[NG][kRedCols];
     __shared__ float red[4];
     const int t = threadIdx.x;
     float sq = 0.0f;
     if (blockIdx.x < a.small_wgs) {
-        const uint32_t grp = t >> 6, per = a.tiles / 4;
+        const uint32_t grp = t / kRedCols;
+        const uint32_t lo = grp * a.tiles / NG, hi = (grp + 1) * a.tiles / NG;
         const uint32_t stat0 = a.float_group + a.head_count;
-        for (uint32_t c0 = blockIdx.x * 64; c0 < stat0 + 5; c0 += a.small_wgs * 64) {
-            const uint32_t col = c0 + (t & 63);
+        for (uint32_t c0 = blockIdx.x * kRedCols; c0 < stat0 + 5; c0 += a.small_wgs * kRedCols) {
+            const uint32_t col = c0 + t % kRedCols;
             float s = 0.0f;
             if (col < stat0 + 5) {
-                const float* src = a.tp + (size_t)grp * per * a.tp_count + col;
+                const float* src = a.tp + col;
                 // loads issued eight at a time, added in tile order
-                for (uint32_t k0 = 0; k0 < per; k0 += 8) {
+                for (uint32_t k0 = lo; k0 < hi; k0 += 8) {
                     float x[8];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) x[u] = k0 + u < per ? src[(size_t)(k0 + u) * a.tp_count] : 0.0f;
+                    for (int u = 0; u < 8; ++u) x[u] = k0 + u < hi ? src[(size_t)(k0 + u) * a.tp_count] : 0.0f;
 #pragma unroll
                     for (int u = 0; u < 8; ++u) s += x[u];
                 }
             }
-            part[grp][t & 63] = s;
+            part[grp][t % kRedCols] = s;
             __syncthreads();
-            if (t < 64 && col < stat0 + 5) {
-                const float g = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+            if (t < kRedCols && col < stat0 + 5) {
+                float g = 0.0f;
+#pragma unroll
+                for (int q = 0; q < NG; ++q) g += part[q][t];
                 if (col < a.float_group) {
                     a.grad[col] = g;
                     sq += g * g;
@@ -826,9 +831,9 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         ga.head_count = E * pv.head_dim;
         ga.mb_stats = mb_stats;
         ga.inv_rows = 1.0f / (float)B;
-        // 64 tile-partial columns per small workgroup, at most half the grid
-        const uint32_t cols = pv.float_group + E * pv.head_dim + 5;
-        ga.small_wgs = (cols + 63) / 64 < kReduceBlocks / 2 ? (cols + 63) / 64 : kReduceBlocks / 2;
+        // kRedCols tile-partial columns per small workgroup, at most half the grid
+        const uint32_t cols = pv.float_group + E * pv.head_dim + 5, cw = dev::kRedCols;
+        ga.small_wgs = (cols + cw - 1) / cw < kReduceBlocks / 2 ? (cols + cw - 1) / cw : kReduceBlocks / 2;
         hipLaunchKernelGGL(dev::grad_reduce_kernel, dim3(kReduceBlocks), dim3(256), 0, st, ga);
         MG_HIP(hipGetLastError(), "grad reduce launch");
     }
