@@ -631,19 +631,41 @@ struct AdamArgs {
     float lr, beta1_pow, beta2_pow, max_grad_norm;
 };
 
+// One parameter's Adam inputs, loaded before the global norm is known so the
+// two memory latencies overlap.
+struct AdamIn {
+    float g, m, v, p;
+};
+__device__ __forceinline__ AdamIn adam_load(const AdamArgs& a, uint32_t i) {
+    return AdamIn{a.grad[i], a.mom[i], a.var[i], a.param[i]};
+}
+
 // model/optimizer.metal:36-60 for element i with the clip scale applied.
-__device__ __forceinline__ float adam_elem(const AdamArgs& a, uint32_t i, float scale) {
+__device__ __forceinline__ float adam_elem(const AdamArgs& a, uint32_t i, const AdamIn& in, float scale) {
     const float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f;
-    const float g = a.grad[i] * scale;
-    const float m = beta1 * a.mom[i] + (1.0f - beta1) * g;
-    const float v = beta2 * a.var[i] + (1.0f - beta2) * g * g;
+    const float g = in.g * scale;
+    const float m = beta1 * in.m + (1.0f - beta1) * g;
+    const float v = beta2 * in.v + (1.0f - beta2) * g * g;
     a.mom[i] = m;
     a.var[i] = v;
     const float mHat = m / (1.0f - a.beta1_pow);
     const float vHat = v / (1.0f - a.beta2_pow);
-    const float p = a.param[i] - a.lr * mHat / (sqrtf(vHat) + eps);
+    const float p = in.p - a.lr * mHat / (sqrtf(vHat) + eps);
     a.param[i] = p;
     return p;
+}
+
+// Every wave adds the kReduceBlocks partial norms in the same order, so all
+// workgroups see the same norm without synchronising with each other; returns
+// the clip scale (model/optimizer.metal:49) and workgroup 0 records the norm.
+__device__ __forceinline__ float adam_clip_scale(const AdamArgs& a) {
+    const int lane = threadIdx.x & 63;
+    float ns = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kReduceBlocks / 64; ++k) ns += a.normpart[lane + 64 * k];
+    const float norm = sqrtf(group_sum<64>(ns));
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.mb_stats[5] = norm;
+    return (a.max_grad_norm > 0.0f && norm > a.max_grad_norm) ? a.max_grad_norm / (norm + 1e-6f) : 1.0f;
 }
 
 // Workgroups [0, mat_tiles) update one 32 x 32 block-matrix tile each and
@@ -651,30 +673,34 @@ __device__ __forceinline__ float adam_elem(const AdamArgs& a, uint32_t i, float 
 // the head elementwise. Workgroup 0 also records the pre-clip norm.
 __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
     __shared__ float lds[kTT * kTileLd];
-    // Every wave adds the kReduceBlocks partial norms in the same order, so all
-    // workgroups see the same norm without synchronising with each other.
-    const int t = threadIdx.x, lane = t & 63;
-    float ns = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kReduceBlocks / 64; ++k) ns += a.normpart[lane + 64 * k];
-    const float norm = sqrtf(group_sum<64>(ns));
-    if (blockIdx.x == 0 && t == 0) a.mb_stats[5] = norm;
-    const float scale =
-        (a.max_grad_norm > 0.0f && norm > a.max_grad_norm) ? a.max_grad_norm / (norm + 1e-6f) : 1.0f;
+    constexpr int PER = kTT * kTT / 256;  // tile elements per thread
+    const int t = threadIdx.x;
     if (blockIdx.x < a.mat_tiles) {
         const MatTile m = mat_tile(blockIdx.x, a.float_group, a.hidden);
         const int c = t & (kTT - 1);
+        uint32_t idx[PER];
+        AdamIn in[PER];
 #pragma unroll
-        for (int e = 0; e < kTT * kTT / 256; ++e) {
+        for (int e = 0; e < PER; ++e) {
             const int r = (256 / kTT) * e + t / kTT;
-            lds[r * kTileLd + c] = adam_elem(a, m.base + (m.r0 + r) * m.cols + m.c0 + c, scale);
+            idx[e] = m.base + (m.r0 + r) * m.cols + m.c0 + c;
+            in[e] = adam_load(a, idx[e]);
+        }
+        const float scale = adam_clip_scale(a);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int r = (256 / kTT) * e + t / kTT;
+            lds[r * kTileLd + c] = adam_elem(a, idx[e], in[e], scale);
         }
         store_tile_t(m, lds, a.param_t);
         return;
     }
     const uint32_t j = (blockIdx.x - a.mat_tiles) * 256 + t;
     const uint32_t i = j < a.float_group ? j : a.off_head + (j - a.float_group);
-    if (i < a.count) adam_elem(a, i, scale);
+    AdamIn in{};
+    if (i < a.count) in = adam_load(a, i);
+    const float scale = adam_clip_scale(a);
+    if (i < a.count) adam_elem(a, i, in, scale);
 }
 
 }  // namespace dev
