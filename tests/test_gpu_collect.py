@@ -60,6 +60,47 @@ def test_collect_teacher_forced(mg, orc, env, n, T):
     run_collect_parity(mg, orc, env, n, T)
 
 
+def test_collect_full_size_subset(mg, orc):
+    """The headline configuration (262144 CartPole envs, T = 32): two collects on
+    the GPU; the oracle replays 1536 of the envs (first, last and a random
+    spread) teacher-forced from the same seeds. Envs are independent, so the
+    subset must match bit for bit (values 1e-4); GAE is checked bit for bit over
+    all envs on the GPU's own inputs."""
+    eid, kernel = ENVS["cartpole"]
+    n, T = 262144, 32
+    gym = mg.Gym(kernel, n, 0)
+    model = mg.PPOModel(gym, horizon=T)
+    d = orc.dims(eid)
+    params = orc.init_params(d, 0)
+    rs = np.random.default_rng(17)
+    idx = np.unique(np.concatenate([[0, 1, 63, 64, n // 2, n - 65, n - 1], rs.choice(n, 1529, replace=False)]))
+    full = orc.GymState(eid, n, 0)
+    g = orc.GymState(eid, idx.size, 0)
+    sb = full.info.state_bytes
+    g.state[:] = full.state.reshape(n, sb)[idx].ravel()
+    g.rng[:] = full.rng[idx]
+    g.done[:] = full.done[idx]
+    slots = orc.Slots(eid, idx.size, T)
+    for c in range(2):
+        model.collect()
+        s = model.download_slots()
+        head = model.head()
+        orc.collect(g, d, params, T, slots, first=(c == 0), teacher_actions=s["actions"][:, idx], threads=THREADS)
+        tag = f"262144-env collect {c}"
+        assert_bit_exact(s["obs"][:, idx], slots.obs, f"{tag} obs slots")
+        assert_bit_exact(s["reward"][:, idx], slots.reward, f"{tag} rewards")
+        assert_bit_exact(s["done"][:, idx], slots.done, f"{tag} dones")
+        assert_bit_exact(gym.rng()[idx], g.rng, f"{tag} rng")
+        assert_bit_exact(gym.state().reshape(n, sb)[idx].ravel(), g.state, f"{tag} state")
+        assert_close(s["value"][:, idx], slots.value, TOL_HEAD, f"{tag} values")
+        assert_close(s["logp"][:, idx], slots.logp, TOL_HEAD, f"{tag} logp")
+        assert_close(head[idx], slots.head, TOL_HEAD, f"{tag} bootstrap head")
+        adv, ret = orc.gae(s["reward"], s["done"], s["value"], head, gym.act_dim)
+        assert_bit_exact(s["adv"], adv, f"{tag} advantages")
+        assert_bit_exact(s["ret"], ret, f"{tag} returns")
+    assert np.isfinite(s["value"]).all() and np.isfinite(s["logp"]).all()
+
+
 @pytest.mark.parametrize("layers,scale", [(1, 1), (3, 2)])
 def test_collect_other_shapes(mg, orc, layers, scale):
     run_collect_parity(mg, orc, "cartpole", 1024, 4, layers=layers, scale=scale, seed=11, collects=1)

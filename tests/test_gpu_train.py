@@ -187,3 +187,37 @@ def test_full_loop_learns(mg):
         st = model.last_stats()
         assert np.all(np.isfinite(st.as_tuple()))
     assert np.mean(lens[-3:]) > 1.5 * np.mean(lens[:3]), lens
+
+
+def test_full_size_iteration_properties(mg):
+    """The BASELINE full-PPO configuration at full size (262144 envs, T = 32,
+    4 epochs of 4096-row minibatches = 8192 Adam steps): every epoch visits each
+    block once, every minibatch's LossStats are finite and in range, the weights
+    stay finite, and a second model from the same seed reproduces the run bit
+    for bit (every reduction has a fixed order)."""
+    n, T, epochs = 262144, 32, 4
+    blocks = T * n // 4096
+
+    def run():
+        gym = mg.Gym("rollout_cartpole", n, 0)
+        model = mg.PPOModel(gym, horizon=T)
+        model.collect()
+        model.train(epochs)
+        return model
+
+    a = run()
+    order = a.last_order()
+    assert order.size == epochs * blocks
+    for e in range(epochs):
+        assert np.array_equal(np.sort(order[e * blocks:(e + 1) * blocks]), np.arange(blocks)), f"epoch {e}"
+    st = a.train_stats()
+    assert st.shape == (epochs * blocks, 6)
+    assert np.isfinite(st).all()
+    assert (st[:, 4] >= 0).all() and (st[:, 4] <= 1).all()      # clip fraction
+    assert (st[:, 1] >= 0).all() and (st[:, 5] >= 0).all()      # value loss, grad norm
+    assert (st[:, 2] >= 0).all() and (st[:, 2] <= np.log(2) + 1e-6).all()  # categorical(2) entropy
+    pa = a.params()
+    assert np.isfinite(pa).all()
+    b = run()
+    assert np.array_equal(b.params().view(np.uint32), pa.view(np.uint32)), "rerun differs"
+    assert np.array_equal(b.train_stats().view(np.uint32), st.view(np.uint32)), "rerun LossStats differ"
