@@ -1,5 +1,5 @@
 // collect<Env>: the whole rollout of model/ppo.h:716-751 (minus GAE) in one
-// launch. Each 256-thread workgroup owns M envs for all T steps:
+// launch. Each workgroup (4 waves; 8 for 16-row tiles) owns M envs for all T steps:
 //
 //   for t in 0..T:  policy forward on the staged obs (MFMA, see policy.h)
 //                   t <  T: env lanes sample from the head with their own RNG,
@@ -17,24 +17,38 @@
 namespace mg {
 namespace dev {
 
+// Launch shape per tile height: 64- and 32-row tiles run 4 waves and two
+// workgroups per CU; 16-row tiles (runs of at most 512 workgroups, one per CU)
+// of envs with up to 16 observation floats run 8 waves with the weights staged
+// through per-wave LDS scratch (a wider observation held by the env lane would
+// not fit the register budget of 8 waves beside the staged weights).
+template <int M, int O>
+struct CollectShape {
+    static constexpr bool STAGE = M == 16 && O <= 16;
+    static constexpr int W = STAGE ? 8 : 4;
+    static constexpr int NT = 64 * W;
+    static constexpr int SCRATCH = STAGE ? W * Shape<M, W>::SW * kEmbed : 1;  // floats
+};
+
 template <int M, int O, int HD>
 struct CollectSmem {
     FwdSmem<M> fwd;
     float obs[M * O];
     float head[M * HD];
+    float wscr[CollectShape<M, O>::SCRATCH];
 };
 
-// 64- and 32-row tiles run two workgroups per CU; 16-row tiles serve runs of
-// at most 512 workgroups and get the whole register file instead.
 template <typename Env, int M>
-__global__ void __launch_bounds__(256, M == 16 ? 1 : 2) collect_kernel(const mg_collect_args a) {
+__global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (M == 16 ? 1 : 2))
+    collect_kernel(const mg_collect_args a) {
     using Tr = EnvTraits<Env>;
     using State = typename Env::State;
     using Action = typename Env::Action;
     using Obs = typename Env::Obs;
+    using CS = CollectShape<M, Env::OBS_DIM>;
     constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
     __shared__ CollectSmem<M, O, HD> sm;
-    FwdRegs<M> R;
+    FwdRegs<M, CS::W> R;
 
     const int tid = threadIdx.x;
     const uint32_t n = a.n, T = a.horizon;
@@ -81,7 +95,7 @@ __global__ void __launch_bounds__(256, M == 16 ? 1 : 2) collect_kernel(const mg_
     __syncthreads();
 
     for (uint32_t t = 0; t <= T; ++t) {
-        policy_forward<M>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
+        policy_forward<M, CS::W, CS::STAGE>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD, sm.wscr);
         if (envLane) {
             const float* h = sm.head + tid * HD;
             if (t == T) {  // bootstrap head for GAE and headValue()
@@ -133,11 +147,11 @@ int launch_collect(const mg_collect_args* a) {
     // n / 64 >= 512 workgroups (2 per CU) to fill the chip. Smaller runs use
     // 32-row, then 16-row tiles for more workgroups.
     if (a->n >= 64u * 512u) {
-        hipLaunchKernelGGL((collect_kernel<Env, 64>), dim3(a->n / 64), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL((collect_kernel<Env, 64>), dim3(a->n / 64), dim3(CollectShape<64, Env::OBS_DIM>::NT), 0, st, *a);
     } else if (a->n >= 32u * 256u) {
-        hipLaunchKernelGGL((collect_kernel<Env, 32>), dim3(a->n / 32), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL((collect_kernel<Env, 32>), dim3(a->n / 32), dim3(CollectShape<32, Env::OBS_DIM>::NT), 0, st, *a);
     } else {
-        hipLaunchKernelGGL((collect_kernel<Env, 16>), dim3(a->n / 16), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL((collect_kernel<Env, 16>), dim3(a->n / 16), dim3(CollectShape<16, Env::OBS_DIM>::NT), 0, st, *a);
     }
     return (int)hipGetLastError();
 }

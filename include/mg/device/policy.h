@@ -509,11 +509,19 @@ __device__ __forceinline__ void fwd_head(const float* Wh, FwdSmem<M, NV>& sm, fl
 }
 
 // Whole forward: obs staged in obsL ([M][O], LDS) -> head in headL ([M][HD], LDS).
-template <int M, int W = 4>
+// With STAGE (16-row tiles) the weights go through the per-wave LDS scratch of
+// LStream (W * SW * 128 floats at wscr); otherwise they stream into registers.
+template <int M, int W = 4, bool STAGE = false>
 __device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem<M>& sm, FwdRegs<M, W>& R,
-                                               const float* obsL, int O, float* headL, int HD) {
-    WStream<M, W> ws;
-    fwd_start<M, W>(pv, ws);
+                                               const float* obsL, int O, float* headL, int HD,
+                                               float* wscr = nullptr) {
+    using Stream = typename std::conditional<STAGE, LStream<M, W>, WStream<M, W>>::type;
+    Stream ws;
+    const int NC = (int)pv.hidden / kChunk;
+    if constexpr (STAGE)
+        ws.start(2 * (int)pv.layers * NC, FwdSeq{&pv, NC}, wscr + (threadIdx.x >> 6) * Shape<M, W>::SW * kEmbed);
+    else
+        ws.start(2 * (int)pv.layers * NC, FwdSeq{&pv, NC});
     fwd_embed<M, W>(pv, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
         fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l]);
