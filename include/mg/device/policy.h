@@ -347,18 +347,6 @@ __device__ __forceinline__ void store_tile(const AccTile<M, W>& acc, float* lds)
     });
 }
 
-// The same, and also to global memory at global[row * ld + gcol0 + col].
-template <int M, int W = 4, bool RELU = false>
-__device__ __forceinline__ void store_tile_g(const AccTile<M, W>& acc, float* lds, float* global, size_t ld,
-                                             int gcol0) {
-    for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
-        float x = acc[rt][ct][r];
-        if (RELU) x = x > 0.0f ? x : 0.0f;
-        lds[row * kLds + col] = x;
-        global[(size_t)row * ld + gcol0 + col] = x;
-    });
-}
-
 // Copies an LDS tile ([M][128], row stride kLds) to global memory
 // (global[row * ld + col]) as float4 rows, NT threads.
 template <int M, int NT>
@@ -477,13 +465,6 @@ __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSm
         if constexpr (VOUT) copy_rows_g<M, S::NT>(vs, v_out + kChunk * c, H);
         ws.template gemm<1>(R.h, vs, s + 1, seq);
     }
-}
-
-// Starts the forward GEMM sequence.
-template <int M, int W = 4>
-__device__ __forceinline__ void fwd_start(const mg_policy_view& pv, WStream<M, W>& ws) {
-    const int NC = (int)pv.hidden / kChunk;
-    ws.start(2 * (int)pv.layers * NC, FwdSeq{&pv, NC});
 }
 
 // model/linear.metal:17-37: head[row][j] = sum_k xs[row][k] W_head[k][j] for

@@ -36,11 +36,6 @@
 
 namespace mg {
 
-MG_HD double bits_to_double(uint64_t b) {
-    union { uint64_t u; double d; } v;
-    v.u = b;
-    return v.d;
-}
 MG_HD uint32_t float_to_bits(float f) {
     union { float f; uint32_t u; } v;
     v.f = f;
@@ -52,69 +47,8 @@ MG_HD float bits_to_float(uint32_t b) {
     return v.f;
 }
 
-// 2^k for k in [-1022, 1023], exact.
-MG_HD double pow2_d(int k) { return bits_to_double((uint64_t)(k + 1023) << 52); }
-
 // Round-half-away-from-zero to an integer, for arguments well inside int range.
 MG_HD int round_to_int(double x) { return x >= 0.0 ? (int)(x + 0.5) : -(int)(-x + 0.5); }
-
-constexpr double kLn2Hi = 6.93147180369123816490e-01;  // high part, exact in few bits
-constexpr double kLn2Lo = 1.90821492927058770002e-10;  // ln2 - kLn2Hi
-constexpr double kInvLn2 = 1.44269504088896338700e+00;
-constexpr double kLn2 = 6.93147180559945286227e-01;
-
-// e^r for |r| <= ln2/2 by Taylor series (Horner), degree 13.
-MG_HD double exp_taylor_d(double r) {
-    double p = 1.0 / 6227020800.0;  // 1/13!
-    p = p * r + 1.0 / 479001600.0;  // 1/12!
-    p = p * r + 1.0 / 39916800.0;
-    p = p * r + 1.0 / 3628800.0;
-    p = p * r + 1.0 / 362880.0;
-    p = p * r + 1.0 / 40320.0;
-    p = p * r + 1.0 / 5040.0;
-    p = p * r + 1.0 / 720.0;
-    p = p * r + 1.0 / 120.0;
-    p = p * r + 1.0 / 24.0;
-    p = p * r + 1.0 / 6.0;
-    p = p * r + 0.5;
-    p = p * r + 1.0;
-    p = p * r + 1.0;
-    return p;
-}
-
-// e^x in double for |x| < 700.
-MG_HD double exp_d(double x) {
-    int k = round_to_int(x * kInvLn2);
-    double r = (x - (double)k * kLn2Hi) - (double)k * kLn2Lo;
-    return exp_taylor_d(r) * pow2_d(k);
-}
-
-// e^y - 1 in double.
-MG_HD double expm1_d(double y) {
-    if (y > -0.5 && y < 0.5) {
-        // Taylor series y + y^2/2! + ... + y^18/18!
-        double p = 1.0 / 6402373705728000.0;  // 1/18!
-        p = p * y + 1.0 / 355687428096000.0;
-        p = p * y + 1.0 / 20922789888000.0;
-        p = p * y + 1.0 / 1307674368000.0;
-        p = p * y + 1.0 / 87178291200.0;
-        p = p * y + 1.0 / 6227020800.0;
-        p = p * y + 1.0 / 479001600.0;
-        p = p * y + 1.0 / 39916800.0;
-        p = p * y + 1.0 / 3628800.0;
-        p = p * y + 1.0 / 362880.0;
-        p = p * y + 1.0 / 40320.0;
-        p = p * y + 1.0 / 5040.0;
-        p = p * y + 1.0 / 720.0;
-        p = p * y + 1.0 / 120.0;
-        p = p * y + 1.0 / 24.0;
-        p = p * y + 1.0 / 6.0;
-        p = p * y + 0.5;
-        p = p * y + 1.0;
-        return p * y;
-    }
-    return exp_d(y) - 1.0;
-}
 
 constexpr double kTwoOverPi = 6.36619772367581382433e-01;
 constexpr double kPio2_1 = 1.57079632673412561417e+00;   // first 33 bits of pi/2
@@ -170,7 +104,6 @@ MG_HD int round_to_int_f(float x) { return x >= 0.0f ? (int)(x + 0.5f) : -(int)(
 constexpr float kLn2HiF = 0.693359375f;         // 355/512: k * kLn2HiF is exact for |k| < 2^15
 constexpr float kLn2LoF = -2.12194440e-4f;      // ln2 - kLn2HiF
 constexpr float kInvLn2F = 1.44269502162933349609f;
-constexpr float kLn2F = 0.693147182464599609375f;
 
 // e^r for |r| <= 0.35 by Taylor series (Horner), degree 7.
 MG_HD float exp_taylor_f(float r) {
