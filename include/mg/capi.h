@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MG_ABI_VERSION 2
+#define MG_ABI_VERSION 3
 #define MG_MAX_LAYERS 8
 #define MG_EMBED 128 /* the reference's N_EMBED_CFG (model/config.h:7) */
 
@@ -99,12 +99,20 @@ typedef struct mg_rollout_args {
  * (columns < act: logits or means, column act: value).
  * params_t holds the block matrices again, transposed, at the same offsets:
  * up^T [hidden x 128] at off_up[l], down^T [128 x hidden] at off_down[l]
- * (other entries unused). The library derives it from params at creation, in
- * every Adam step and in mg_ppo_set_params / mg_ppo_params_updated; the
- * fused forward reads the matrices from it. */
+ * (other entries unused). frag_fwd and frag_bwd hold them once more in the
+ * operand order of 16x16x4 matrix instructions: a matrix read as rows n of
+ * contraction length K is cut into 16 x 128 tiles, and element (n, k) sits at
+ * (n / 16) 16 K + (k / 128) 2048 + (k % 128 / 16) 256 + (k % 16 / 4) 64 +
+ * (n % 16) 4 + k % 4 from the matrix's offset. frag_fwd holds up^T and down^T
+ * (the forward's operands), frag_bwd up and down as stored (the backward's).
+ * The library derives all three from params at creation, in every Adam step
+ * and in mg_ppo_set_params / mg_ppo_params_updated; the fused kernels read
+ * the matrices from them. */
 typedef struct mg_policy_view {
     float* params;
     float* params_t;
+    float* frag_fwd;
+    float* frag_bwd;
     uint32_t obs_dim;
     uint32_t act_dim;
     uint32_t embed;

@@ -19,15 +19,13 @@ namespace dev {
 
 // Launch shape per tile height: 64- and 32-row tiles run 4 waves and two
 // workgroups per CU; 16-row tiles (runs of at most 512 workgroups, one per CU)
-// of envs with up to 16 observation floats run 8 waves with the weights staged
-// through per-wave LDS scratch (a wider observation held by the env lane would
-// not fit the register budget of 8 waves beside the staged weights).
+// of envs with up to 16 observation floats run 8 waves, 16 output columns each
+// (a wider observation held by the env lane would not fit the register budget
+// of 8 waves).
 template <int M, int O>
 struct CollectShape {
-    static constexpr bool STAGE = M == 16 && O <= 16;
-    static constexpr int W = STAGE ? 8 : 4;
+    static constexpr int W = M == 16 && O <= 16 ? 8 : 4;
     static constexpr int NT = 64 * W;
-    static constexpr int SCRATCH = STAGE ? W * Shape<M, W>::SW * kEmbed : 1;  // floats
 };
 
 template <int M, int O, int HD>
@@ -35,7 +33,6 @@ struct CollectSmem {
     FwdSmem<M> fwd;
     float obs[M * O];
     float head[M * HD];
-    float wscr[CollectShape<M, O>::SCRATCH];
 };
 
 template <typename Env, int M>
@@ -95,7 +92,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (M == 16 
     __syncthreads();
 
     for (uint32_t t = 0; t <= T; ++t) {
-        policy_forward<M, CS::W, CS::STAGE>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD, sm.wscr);
+        policy_forward<M, CS::W>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
         if (envLane) {
             const float* h = sm.head + tid * HD;
             if (t == T) {  // bootstrap head for GAE and headValue()

@@ -255,60 +255,60 @@ struct WStream {
     }
 };
 
-// Weight stream for 16-row tiles that stages each GEMM's weights through a
-// private LDS scratch of the wave. The MFMA operand layout puts 16 different
-// weight rows (64 B each) in one float4 load, 16 L1 requests per KB; here each
-// load instruction covers two whole 512-byte rows (8 cache lines per KB), the
-// rows go to the wave's scratch XOR-swizzled (slot r * 32 + (c ^ (r & 7)) for
-// row r, 16-byte chunk c), and the GEMM reads them back in MFMA layout without
-// bank conflicts. Only the owning wave touches its scratch, so no barrier is
-// needed: a wave's LDS operations complete in order. Each GEMM writes its
-// weights to the scratch first, then issues the loads of the GEMM two ahead,
-// one per k-group between the MFMAs. (Writing the next GEMM's weights in the
-// middle of this one measured slower: that write waits for loads issued only
-// one GEMM earlier and stalls the MFMAs behind it.) Same interface as WStream.
+// Offset of element (n, k) of a matrix read as rows n of contraction length K
+// (K a multiple of 128) in the fragment-tiled layout of frag_fwd / frag_bwd:
+// 16 x 128 tiles, tile (n / 16, k / 128) at (n / 16) 16 K + (k / 128) 2048, and
+// inside a tile the float4 of lane q 16 + n % 16 for k-group g = k % 128 / 16 at
+// g 256 + (q 16 + n % 16) 4, q = k % 16 / 4. One k-group of one 16-row strip
+// is then 64 consecutive float4s in the lane order of a 16x16x4 B operand.
+__host__ __device__ constexpr uint32_t frag_index(uint32_t n, uint32_t k, uint32_t K) {
+    return (n >> 4) * 16u * K + (k >> 7) * 2048u + ((k & 127u) >> 4) * 256u + ((k & 15u) >> 2) * 64u +
+           (n & 15u) * 4u + (k & 3u);
+}
+
+// Weight stream for 16-row tiles over the fragment-tiled copies: a GEMM's
+// operand for one wave is one 16 x 128 tile per 16 output columns, and each
+// k-group is one float4 per lane from 1 KB of consecutive memory (eight whole
+// cache lines), loaded straight into the MFMA registers. Two whole fragments,
+// one per GEMM role, each refilled two GEMMs ahead one k-group at a time right
+// after that k-group's MFMAs; past the end of the sequence a GEMM reloads its
+// own operand, so every path issues the same loads. A FragSrc here points at
+// the tile of the chunk's first output column and ld is the matrix's
+// contraction length K (16-row strips are 16 K floats apart).
 template <int M, int W>
-struct LStream {
+struct TStream {
     using S = Shape<M, W>;
-    static_assert(S::MT == 16 && S::SW % 2 == 0, "16x16x4 tiles, two rows per load");
-    static constexpr int NI = S::SW / 2;        // raw float4 loads per lane per GEMM
+    static_assert(S::MT == 16 && S::KG == 16, "16x16x4 tiles");
     static constexpr int NGF = kEmbed / S::KG;  // k-groups of one 128-deep GEMM
-    static_assert(NI <= NGF, "one refill load per k-group at most");
-    f32x4 raw[2][NI];
-    float* scr;  // this wave's scratch: SW rows x 128 floats
+    BFrag<M, W, NGF> b[2];
     int total;
 
-    __device__ __forceinline__ void load_raw(int role, const FragSrc& f, int i) {
-        const int lane = threadIdx.x & 63, n0 = S::SW * (threadIdx.x >> 6);
-        raw[role][i] = *reinterpret_cast<const f32x4*>(f.p + (size_t)(n0 + 2 * i + (lane >> 5)) * f.ld +
-                                                       4 * (lane & 31));
+    static __device__ __forceinline__ const float* lane_ptr(const FragSrc& f, int ct) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        return f.p + (size_t)(wave * S::CT + ct) * 16 * f.ld + 4 * lane;
     }
-    static __device__ __forceinline__ int slot(int r, int c) { return r * 32 + (c ^ (r & 7)); }
-    __device__ __forceinline__ void write_scratch(int role) {
-        const int lane = threadIdx.x & 63;
+    static __device__ __forceinline__ void load_group(BFrag<M, W, NGF>& f, const FragSrc& src, int g) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int r = 2 * i + (lane >> 5);
-            *reinterpret_cast<f32x4*>(scr + 4 * slot(r, lane & 31)) = raw[role][i];
+        for (int ct = 0; ct < S::CT; ++ct) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(lane_ptr(src, ct) + 256 * g);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
         }
     }
 
-    // n >= 2 GEMMs; scratch = SW * 128 floats of LDS owned by this wave.
     template <class Src>
-    __device__ __forceinline__ void start(int n, Src src, float* scratch) {
+    __device__ __forceinline__ void start(int n, Src src) {
         total = n;
-        scr = scratch;
         const FragSrc f0 = src(0), f1 = src(1);
 #pragma unroll
-        for (int i = 0; i < NI; ++i) load_raw(0, f0, i);
+        for (int g = 0; g < NGF; ++g) load_group(b[0], f0, g);
 #pragma unroll
-        for (int i = 0; i < NI; ++i) load_raw(1, f1, i);
+        for (int g = 0; g < NGF; ++g) load_group(b[1], f1, g);
     }
 
     template <int ROLE, class Src>
     __device__ __forceinline__ void gemm(AccTile<M, W>& acc, const float* a_lds, int s, Src src) {
         const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane);
-        write_scratch(ROLE);
         const FragSrc f = src(s + 2 < total ? s + 2 : s);
         const float* ap = a_lds + n * kLds + 4 * q;
         f32x4 a[NGF][S::RT];
@@ -317,12 +317,6 @@ struct LStream {
 #pragma unroll
             for (int rt = 0; rt < S::RT; ++rt)
                 a[g][rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
-        f32x4 b[NGF][S::CT];
-#pragma unroll
-        for (int g = 0; g < NGF; ++g)
-#pragma unroll
-            for (int ct = 0; ct < S::CT; ++ct)
-                b[g][ct] = *reinterpret_cast<const f32x4*>(scr + 4 * slot(n + S::MT * ct, 4 * g + q));
 #pragma unroll
         for (int g = 0; g < NGF; ++g) {
 #pragma unroll
@@ -330,8 +324,9 @@ struct LStream {
 #pragma unroll
                 for (int rt = 0; rt < S::RT; ++rt)
 #pragma unroll
-                    for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[g][rt][j], b[g][ct][j], acc[rt][ct]);
-            if (g < NI) load_raw(ROLE, f, g);
+                    for (int ct = 0; ct < S::CT; ++ct)
+                        acc[rt][ct] = S::mfma(a[g][rt][j], b[ROLE].b[g][ct][j], acc[rt][ct]);
+            load_group(b[ROLE], f, g);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -440,6 +435,19 @@ struct FwdSeq {
     }
 };
 
+// The same sequence over the fragment-tiled copies in frag_fwd (for TStream):
+// Up^T rows c (K = 128) start at tile row 128 c / 16, Down^T's chunk c (K = H)
+// at tile column c.
+struct FwdSeqF {
+    const mg_policy_view* pv;
+    int nc;
+    __device__ __forceinline__ FragSrc operator()(int s) const {
+        const int l = s / (2 * nc), c = (s >> 1) % nc;
+        if ((s & 1) == 0) return {pv->frag_fwd + pv->off_up[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
+        return {pv->frag_fwd + pv->off_down[l] + 16 * kChunk * c, pv->hidden};
+    }
+};
+
 // One residual block (model/mlp.metal:18-86 + model/elementwise.metal:4-13):
 // h += relu(xs Up) Down, the hidden dimension in 128-wide chunks whose Down
 // products accumulate straight into the residual stream (the residual add
@@ -452,7 +460,7 @@ __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSm
                                           Stream& ws, float* v_out = nullptr, Seq seq = Seq{}) {
     using S = Shape<M, W>;
     const int H = (int)pv.hidden, NC = H / kChunk;
-    if constexpr (std::is_same<Seq, FwdSeq>::value) seq = FwdSeq{&pv, NC};
+    if constexpr (std::is_same<Seq, FwdSeq>::value || std::is_same<Seq, FwdSeqF>::value) seq = Seq{&pv, NC};
     for (int c = 0; c < NC; ++c) {
         const int s = 2 * (l * NC + c);
         float* vs = sm.vs[NV == 2 ? (c & 1) : 0];
@@ -490,23 +498,22 @@ __device__ __forceinline__ void fwd_head(const float* Wh, FwdSmem<M, NV>& sm, fl
 }
 
 // Whole forward: obs staged in obsL ([M][O], LDS) -> head in headL ([M][HD], LDS).
-// With STAGE (16-row tiles) the weights go through the per-wave LDS scratch of
-// LStream (W * SW * 128 floats at wscr); otherwise they stream into registers.
-template <int M, int W = 4, bool STAGE = false>
+// 16-row tiles read the fragment-tiled copies (TStream); taller tiles stream
+// half-fragments of the transposed copies (WStream).
+template <int M, int W = 4>
 __device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem<M>& sm, FwdRegs<M, W>& R,
-                                               const float* obsL, int O, float* headL, int HD,
-                                               float* wscr = nullptr) {
-    using Stream = typename std::conditional<STAGE, LStream<M, W>, WStream<M, W>>::type;
-    Stream ws;
+                                               const float* obsL, int O, float* headL, int HD) {
+    constexpr bool TILED = M == 16;
+    using Stream = typename std::conditional<TILED, TStream<M, W>, WStream<M, W>>::type;
+    using Seq = typename std::conditional<TILED, FwdSeqF, FwdSeq>::type;
     const int NC = (int)pv.hidden / kChunk;
-    if constexpr (STAGE)
-        ws.start(2 * (int)pv.layers * NC, FwdSeq{&pv, NC}, wscr + (threadIdx.x >> 6) * Shape<M, W>::SW * kEmbed);
-    else
-        ws.start(2 * (int)pv.layers * NC, FwdSeq{&pv, NC});
+    const Seq seq{&pv, NC};
+    Stream ws;
+    ws.start(2 * (int)pv.layers * NC, seq);
     fwd_embed<M, W>(pv, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
         fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l]);
-        fwd_block<M, W>(pv, (int)l, sm, R, ws);
+        fwd_block<M, W, false, 1, Seq>(pv, (int)l, sm, R, ws, nullptr, seq);
     }
     fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[pv.layers], pv.params + pv.off_ln_beta[pv.layers]);
     fwd_head<M, W>(pv.params + pv.off_head, sm, headL, HD);

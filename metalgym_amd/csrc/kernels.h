@@ -46,7 +46,8 @@ struct TrainStep {
     float beta1_pow, beta2_pow;
 };
 
-// params_t (the transposed block matrices) from params.
+// params_t (the transposed block matrices) and the fragment-tiled copies
+// (frag_fwd, frag_bwd) from params.
 int launch_transpose_blocks(hipStream_t st, const mg_policy_view& pv);
 // MG_OK if the block matrices sit contiguously from float_group (the layout
 // the Adam and transpose kernels tile).

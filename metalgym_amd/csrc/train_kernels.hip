@@ -135,15 +135,16 @@ __device__ __forceinline__ void bwd_layernorm(TSmem& sm, TRegs& G, const float* 
 // The backward's GEMM sequence, blocks in reverse: for block l and chunk c,
 // GEMM 2 ((L - 1 - l) NC + c) is dV_c = dh Down[c, :]^T (weights Down rows c,
 // [128 hidden][128]) and the next one is dx += dV_c Up[:, c]^T (weights Up
-// columns c, [128][H]); both are the arena's own row-major matrices read as
-// transposed operands.
+// columns c, [128][H]), both from the fragment-tiled copies of the matrices as
+// stored (frag_bwd): Down rows c (K = 128) start at tile row 128 c / 16, Up's
+// chunk c (K = H) at tile column c.
 struct BwdSeq {
     const mg_policy_view* pv;
     int nc;
     __device__ __forceinline__ FragSrc operator()(int s) const {
         const int l = (int)pv->layers - 1 - s / (2 * nc), c = (s >> 1) % nc;
-        if ((s & 1) == 0) return {pv->params + pv->off_down[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
-        return {pv->params + pv->off_up[l] + kChunk * c, pv->hidden};
+        if ((s & 1) == 0) return {pv->frag_bwd + pv->off_down[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
+        return {pv->frag_bwd + pv->off_up[l] + 16 * kChunk * c, pv->hidden};
     }
 };
 
@@ -155,15 +156,14 @@ struct TrainSeq {
     int nc;
     __device__ __forceinline__ FragSrc operator()(int s) const {
         const int F = 2 * (int)pv->layers * nc;
-        return s < F ? FwdSeq{pv, nc}(s) : BwdSeq{pv, nc}(s - F);
+        return s < F ? FwdSeqF{pv, nc}(s) : BwdSeq{pv, nc}(s - F);
     }
 };
 
 // Backward of block l (model/mlp.metal:88-153 + model/ppo.h:851-852). D holds
 // the gradient at the block output (dStream) and is updated in place to the
 // gradient at the block input. Chunked like the forward: dV_c = (dh Down_c^T)
-// masked by relu, then dx += dV_c Up_c^T; both weight reads are contiguous
-// float4s along the contraction; ws streams the row pass's TrainSeq.
+// masked by relu, then dx += dV_c Up_c^T; ws streams the row pass's TrainSeq.
 template <class Stream>
 __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem& sm, TRegs& D,
                                           Stream& ws, const float* v_tile, float* dv_store, float* dh_store,
@@ -203,42 +203,26 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem
         for (int ct = 0; ct < TS::CT; ++ct) D.h[rt][ct] = G.h[rt][ct] + D.h[rt][ct];  // residualAdd(dBranch, dStream)
 }
 
-// Size classes of the row pass. Staged: LDS-staged weights (LStream) for up to
-// 4 blocks, obs <= 32 and head <= 16 floats, which leaves room for the 64 KB of
-// per-wave weight scratch; Wide: any supported shape, weights streamed straight
-// into registers (WStream).
-struct RowsStaged {
-    static constexpr int LMAX = 4, OMAX = 32, HDMAX = 16;
-    static constexpr bool STAGE = true;
-};
-struct RowsWide {
-    static constexpr int LMAX = MG_MAX_LAYERS, OMAX = kMaxObsT, HDMAX = kMaxHeadT;
-    static constexpr bool STAGE = false;
-};
-
-// LDS of one train_rows workgroup. The LN captures xn / sd are only read by
-// the LN backward, so they never leave the CU.
-template <class Cfg>
+// LDS of one train_rows workgroup, sized for every supported shape. The LN
+// captures xn / sd are only read by the LN backward, so they never leave the CU.
 struct RowsSmem {
     TSmem sm;
-    float xn[(Cfg::LMAX + 1) * kTR * kEmbed];
-    float sd[(Cfg::LMAX + 1) * kTR];
-    float ln[(Cfg::LMAX + 1) * 2 * kEmbed];  // gamma, beta of every LN
-    float wh[kEmbed * Cfg::HDMAX];           // W_head
-    float obs[kTR * Cfg::OMAX];
-    float head[kTR * Cfg::HDMAX];
-    float dhead[kTR * Cfg::HDMAX];
-    float dls[kTR * Cfg::HDMAX];
+    float xn[(MG_MAX_LAYERS + 1) * kTR * kEmbed];
+    float sd[(MG_MAX_LAYERS + 1) * kTR];
+    float ln[(MG_MAX_LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
+    float wh[kEmbed * kMaxHeadT];                // W_head
+    float obs[kTR * kMaxObsT];
+    float head[kTR * kMaxHeadT];
+    float dhead[kTR * kMaxHeadT];
+    float dls[kTR * kMaxHeadT];
     float stat[kTR * 5];
     float scratch[kTNT];
-    float wscr[Cfg::STAGE ? kTNT / 64 * TS::SW * kEmbed : 1];  // per-wave weight scratch
 };
 
-template <class Cfg>
 __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     constexpr int M = kTR;
-    using Stream = typename std::conditional<Cfg::STAGE, LStream<kTR, kTW>, WStream<kTR, kTW>>::type;
-    __shared__ RowsSmem<Cfg> L;
+    using Stream = TStream<kTR, kTW>;
+    __shared__ RowsSmem L;
     TSmem& sm = L.sm;
     TRegs R;
     const mg_policy_view& pv = a.pv;
@@ -272,10 +256,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     }
     Stream wst;
     const TrainSeq seq{&pv, H / kChunk};
-    if constexpr (Cfg::STAGE)
-        wst.start(4 * NL * (H / kChunk), seq, L.wscr + (tid >> 6) * TS::SW * kEmbed);
-    else
-        wst.start(4 * NL * (H / kChunk), seq);
+    wst.start(4 * NL * (H / kChunk), seq);
     __syncthreads();
 
     // ---- forward with capture ----
@@ -604,9 +585,29 @@ __device__ __forceinline__ void store_tile_t(const MatTile& m, const float* lds,
     }
 }
 
-// params_t from params (the transposed block matrices), one tile per workgroup.
+// Writes the tile held in lds ([r][c], stride kTileLd) to the fragment-tiled
+// copies: frag_bwd reads the matrix as stored (rows n = r, contraction k = c,
+// K = cols), frag_fwd its transpose (n = c, k = r, K = rows). Each thread writes
+// one float4 (four consecutive k of one n) to each; a wave's 64 float4s are
+// one 1 KB run. No barrier (the caller has ordered the LDS writes).
+__device__ __forceinline__ void store_tile_frag(const MatTile& m, const float* lds, float* frag_fwd,
+                                                float* frag_bwd) {
+    const int t = threadIdx.x;
+    const int n = 16 * (t >> 7) + (t & 15), k = 16 * ((t >> 6) & 1) + 4 * ((t >> 4) & 3);
+    f32x4 vb, vf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        vb[j] = lds[n * kTileLd + k + j];
+        vf[j] = lds[(k + j) * kTileLd + n];
+    }
+    *reinterpret_cast<f32x4*>(frag_bwd + m.base + frag_index(m.r0 + n, m.c0 + k, m.cols)) = vb;
+    *reinterpret_cast<f32x4*>(frag_fwd + m.base + frag_index(m.c0 + n, m.r0 + k, m.rows)) = vf;
+}
+
+// params_t and the fragment-tiled copies from params, one tile per workgroup.
 __global__ void __launch_bounds__(256) transpose_blocks_kernel(const float* __restrict__ param,
-                                                               float* __restrict__ param_t, uint32_t float_group,
+                                                               float* __restrict__ param_t, float* __restrict__ frag_fwd,
+                                                               float* __restrict__ frag_bwd, uint32_t float_group,
                                                                uint32_t H) {
     __shared__ float lds[kTT * kTileLd];
     const MatTile m = mat_tile(blockIdx.x, float_group, H);
@@ -617,11 +618,14 @@ __global__ void __launch_bounds__(256) transpose_blocks_kernel(const float* __re
         lds[r * kTileLd + c] = param[m.base + (size_t)(m.r0 + r) * m.cols + m.c0 + c];
     }
     store_tile_t(m, lds, param_t);
+    store_tile_frag(m, lds, frag_fwd, frag_bwd);
 }
 
 struct AdamArgs {
     float* param;
     float* param_t;
+    float* frag_fwd;
+    float* frag_bwd;
     const float* grad;
     float* mom;
     float* var;
@@ -669,8 +673,9 @@ __device__ __forceinline__ float adam_clip_scale(const AdamArgs& a) {
 }
 
 // Workgroups [0, mat_tiles) update one 32 x 32 block-matrix tile each and
-// write it transposed to param_t as well; the rest update the vector group and
-// the head elementwise. Workgroup 0 also records the pre-clip norm.
+// write it to param_t and the fragment-tiled copies as well; the rest update
+// the vector group and the head elementwise. Workgroup 0 also records the
+// pre-clip norm.
 __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
     __shared__ float lds[kTT * kTileLd];
     constexpr int PER = kTT * kTT / 256;  // tile elements per thread
@@ -693,6 +698,7 @@ __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
             lds[r * kTileLd + c] = adam_elem(a, idx[e], in[e], scale);
         }
         store_tile_t(m, lds, a.param_t);
+        store_tile_frag(m, lds, a.frag_fwd, a.frag_bwd);
         return;
     }
     const uint32_t j = (blockIdx.x - a.mat_tiles) * 256 + t;
@@ -763,7 +769,7 @@ int train_ws_bind(const mg_policy_view& pv, uint32_t rows, void* base, TrainWs* 
 
 int check_matrix_layout(const mg_policy_view& pv) {
     const uint32_t E = MG_EMBED, H = pv.hidden;
-    MG_CHECK(pv.embed == E && H % 64 == 0, MG_ERR_INVALID, "policy: embed 128 and hidden a multiple of 64 required");
+    MG_CHECK(pv.embed == E && H % 128 == 0, MG_ERR_INVALID, "policy: embed 128 and hidden a multiple of 128 required");
     for (uint32_t l = 0; l < pv.layers; ++l)
         MG_CHECK(pv.off_up[l] == pv.float_group + 2 * l * E * H && pv.off_down[l] == pv.off_up[l] + E * H &&
                      pv.off_head == pv.float_group + 2 * pv.layers * E * H,
@@ -775,7 +781,7 @@ int launch_transpose_blocks(hipStream_t st, const mg_policy_view& pv) {
     int rc = check_matrix_layout(pv);
     if (rc) return rc;
     hipLaunchKernelGGL(dev::transpose_blocks_kernel, dim3(mat_tiles(pv)), dim3(256), 0, st, pv.params, pv.params_t,
-                       pv.float_group, pv.hidden);
+                       pv.frag_fwd, pv.frag_bwd, pv.float_group, pv.hidden);
     MG_HIP(hipGetLastError(), "transpose launch");
     return MG_OK;
 }
@@ -808,13 +814,7 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         ra.logp_slots = logp_slots;
         ra.adv_stats = adv_stats;
         ra.head_out = head_out;
-        if (L <= (uint32_t)dev::RowsStaged::LMAX && pv.obs_dim <= (uint32_t)dev::RowsStaged::OMAX &&
-            pv.head_dim <= (uint32_t)dev::RowsStaged::HDMAX)
-            hipLaunchKernelGGL(dev::train_rows_kernel<dev::RowsStaged>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st,
-                               ra);
-        else
-            hipLaunchKernelGGL(dev::train_rows_kernel<dev::RowsWide>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st,
-                               ra);
+        hipLaunchKernelGGL(dev::train_rows_kernel, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         MG_HIP(hipGetLastError(), "train rows launch");
     }
     {  // 2. block-matrix weight gradients
@@ -868,6 +868,8 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         dev::AdamArgs aa;
         aa.param = pv.params;
         aa.param_t = pv.params_t;
+        aa.frag_fwd = pv.frag_fwd;
+        aa.frag_bwd = pv.frag_bwd;
         aa.grad = ws.grad;
         aa.mom = m;
         aa.var = v;

@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported(mg):
 
 
 def test_abi_version(mg):
-    assert mg.lib().mg_abi_version() == 2
+    assert mg.lib().mg_abi_version() == 3
 
 
 def test_builtin_envs_registered(mg):
