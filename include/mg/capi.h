@@ -97,22 +97,21 @@ typedef struct mg_rollout_args {
  * (Gaussian head only); then per block up [128 x hidden] and down [hidden x 128]
  * (row-major, x @ W), then head [128 x head_dim], head_dim = act + 1
  * (columns < act: logits or means, column act: value).
- * params_t holds the block matrices again, transposed, at the same offsets:
- * up^T [hidden x 128] at off_up[l], down^T [128 x hidden] at off_down[l]
- * (other entries unused). frag_fwd and frag_bwd hold them once more in the
- * operand order of 16x16x4 matrix instructions: a matrix read as rows n of
- * contraction length K is cut into 16 x 128 tiles, and element (n, k) sits at
- * (n / 16) 16 K + (k / 128) 2048 + (k % 128 / 16) 256 + (k % 16 / 4) 64 +
- * (n % 16) 4 + k % 4 from the matrix's offset. frag_fwd holds up^T and down^T
- * (the forward's operands), frag_bwd up and down as stored (the backward's).
- * The library derives all three from params at creation, in every Adam step
- * and in mg_ppo_set_params / mg_ppo_params_updated; the fused kernels read
- * the matrices from them. */
+ * frag_fwd32, frag_fwd16 and frag_bwd16 hold the block matrices again, at
+ * the same offsets, in the operand order of MT x MT matrix instructions: a
+ * matrix read as rows n of contraction length K is cut into MT x 128 tiles,
+ * and element (n, k) sits at (n / MT) MT K + (k / 128) MT 128 +
+ * (k % 128 / KG) 256 + (k % KG / 4) 4 MT + (n % MT) 4 + k % 4 from the
+ * matrix's offset (MT = 32, KG = 8 for 32x32x2; MT = 16, KG = 16 for 16x16x4).
+ * frag_fwd32 and frag_fwd16 hold up^T and down^T (the forward's operands),
+ * frag_bwd16 up and down as stored (the backward's). The library derives them
+ * from params at creation, in every Adam step and in mg_ppo_set_params /
+ * mg_ppo_params_updated; the fused kernels read the matrices from them. */
 typedef struct mg_policy_view {
     float* params;
-    float* params_t;
-    float* frag_fwd;
-    float* frag_bwd;
+    float* frag_fwd32;
+    float* frag_fwd16;
+    float* frag_bwd16;
     uint32_t obs_dim;
     uint32_t act_dim;
     uint32_t embed;
@@ -306,10 +305,11 @@ int mg_ppo_slots_get(mg_ppo* model, mg_ppo_slots* out);
 int mg_ppo_head(mg_ppo* model, const float** head, uint32_t* rows, uint32_t* head_dim);
 int mg_ppo_policy(mg_ppo* model, mg_policy_view* out);
 /* Replaces all parameters (count = mg_policy_view.count floats from host
- * memory) and re-derives params_t. No reference counterpart: the reference's
+ * memory) and re-derives the fragment-tiled copies. No reference counterpart: the reference's
  * weights are shared CPU/GPU memory that tests write in place. */
 int mg_ppo_set_params(mg_ppo* model, const float* host, uint32_t count);
-/* Re-derives params_t after the caller wrote params through the device view. */
+/* Re-derives the fragment-tiled copies after the caller wrote params through
+ * the device view. */
 int mg_ppo_params_updated(mg_ppo* model);
 /* Adam state: first and second moments, same layout as the parameters. */
 int mg_ppo_adam_state(mg_ppo* model, float** m, float** v, uint32_t* step);

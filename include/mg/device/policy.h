@@ -113,22 +113,55 @@ struct BFrag {
     float b[NG][Shape<M, W>::CT][4];
 };
 
-// Loads k-groups [g0, g0 + NG) of a transposed weight operand: W^T element
-// (k, n) at wt_ptr[n * wt_ld + k], so each lane's four k-values are one
-// contiguous float4.
-template <int M, int W, int NG>
-__device__ __forceinline__ void load_frag_t(BFrag<M, W, NG>& f, const float* wt_ptr, size_t wt_ld, int g0) {
+// Offset of element (n, k) of a matrix read as rows n of contraction length K
+// (K a multiple of 128) in the fragment-tiled layout for MT x MT MFMA tiles
+// (MT = 16: 16x16x4, KG = 16 k per float4 group; MT = 32: 32x32x2, KG = 8):
+// strips of MT rows cut into MT x 128 tiles, tile (n / MT, k / 128) at
+// (n / MT) MT K + (k / 128) MT 128, and inside a tile k-group g = k % 128 / KG
+// at g 256 as 64 float4s in lane order, lane q MT + n % MT holding the four
+// k = g KG + 4 q + j, q = k % KG / 4, j = k % 4. One k-group of one strip is
+// then 1 KB of consecutive memory in exactly the lane layout of the B operand.
+template <int MT>
+__host__ __device__ constexpr uint32_t frag_index(uint32_t n, uint32_t k, uint32_t K) {
+    constexpr uint32_t KG = MT == 32 ? 8u : 16u;
+    return (n / MT) * MT * K + (k >> 7) * MT * 128u + ((k & 127u) / KG) * 256u + ((k % KG) >> 2) * MT * 4u +
+           (n % MT) * 4u + (k & 3u);
+}
+
+// Where the s-th weight operand of a GEMM sequence lives: p is the first
+// element of the fragment-tiled strip holding the chunk's first output column
+// at the chunk's first k, ld the matrix's contraction length K.
+struct FragSrc {
+    const float* p;
+    uint32_t ld;
+};
+
+// This lane's float4 of k-group 0 for column tile ct of its wave's strip. The
+// strip's address is wave-uniform (scalar registers), so every weight load is
+// a scalar base plus the one per-lane offset 16 lane bytes.
+template <int M, int W>
+__device__ __forceinline__ const float* frag_lane(const FragSrc& f, int ct) {
     using S = Shape<M, W>;
-    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane), n0 = S::SW * (threadIdx.x >> 6);
-    const float* bp = wt_ptr + (size_t)(n0 + n) * wt_ld + 4 * q + S::KG * g0;
+    const uint32_t lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    return f.p + (size_t)(wave * S::CT + ct) * S::MT * f.ld + 4 * lane;
+}
+
+// Loads k-groups [g0, g0 + NG) of a fragment-tiled operand: one float4 per lane
+// and k-group, each wave instruction one 1 KB run.
+template <int M, int W, int NG>
+__device__ __forceinline__ void load_frag(BFrag<M, W, NG>& f, const FragSrc& src, int g0) {
+    using S = Shape<M, W>;
 #pragma unroll
-    for (int g = 0; g < NG; ++g)
+    for (int ct = 0; ct < S::CT; ++ct) {
+        const float* bp = frag_lane<M, W>(src, ct) + 256 * g0;
 #pragma unroll
-        for (int ct = 0; ct < S::CT; ++ct) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(bp + (size_t)(S::MT * ct) * wt_ld + S::KG * g);
+        for (int g = 0; g < NG; ++g) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(bp + 256 * g);
 #pragma unroll
             for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
         }
+    }
 }
 
 // acc[rt][ct] += A[rows][k-groups g0 .. g0 + NG) @ B for this wave's strip. A
@@ -156,68 +189,15 @@ __device__ __forceinline__ void gemm_frag(AccTile<M, W>& acc, const float* a_lds
                 for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[g][rt][j], f.b[g][ct][j], acc[rt][ct]);
 }
 
-// gemm_frag fused with the refill of the same registers: k-group g's weights
-// are replaced by k-group g of `next` as soon as its MFMAs have issued, so a
-// wave's refill loads leave one at a time over the GEMM instead of as a burst
-// after it (a burst from every wave of the CU backs up the CU's vector-memory
-// address path and stalls the issuing waves).
-template <int M, int W, int NG>
-__device__ __forceinline__ void gemm_frag_refill(AccTile<M, W>& acc, const float* a_lds, BFrag<M, W, NG>& f,
-                                                 const float* next_p, size_t next_ld, int g0) {
-    using S = Shape<M, W>;
-    const int lane = threadIdx.x & 63, n = S::col(lane), q = S::quad(lane), n0 = S::SW * (threadIdx.x >> 6);
-    const float* ap = a_lds + n * kLds + 4 * q + S::KG * g0;
-    const float* bp = next_p + (size_t)(n0 + n) * next_ld + 4 * q + S::KG * g0;
-    f32x4 a[NG][S::RT];
-#pragma unroll
-    for (int g = 0; g < NG; ++g)
-#pragma unroll
-        for (int rt = 0; rt < S::RT; ++rt)
-            a[g][rt] = *reinterpret_cast<const f32x4*>(ap + S::MT * rt * kLds + S::KG * g);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int rt = 0; rt < S::RT; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < S::CT; ++ct) acc[rt][ct] = S::mfma(a[g][rt][j], f.b[g][ct][j], acc[rt][ct]);
-#pragma unroll
-        for (int ct = 0; ct < S::CT; ++ct) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(bp + (size_t)(S::MT * ct) * next_ld + S::KG * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
-        }
-        // keep the interleave: the scheduler would otherwise sink every load
-        // to the end of the GEMM to shorten their live ranges
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// Where the s-th weight operand of a GEMM sequence lives (transposed layout).
-struct FragSrc {
-    const float* p;
-    uint32_t ld;
-};
-
-// Register double buffer for a sequence of 128-deep chunk GEMMs whose weight
-// operands are known in advance (a forward or backward pass). The loads of a
-// later GEMM's weights are issued as soon as registers free up, so their L2
-// latency overlaps the MFMA work (and the barriers) in between instead of
-// stalling every k-group. With whole fragments every GEMM issues the same
-// loads on every path (past the end of the sequence it reloads its own
-// operand): the compiler's vector-memory wait counts are then exact at the
-// chunk loop's head instead of the conservative merge of paths with different
-// numbers of loads in flight.
-//  - 16-row tiles (registers to spare): two whole fragments, one per GEMM
-//    role, each refilled two GEMMs ahead.
-//  - 32/64-row tiles (two workgroups per CU): the two halves of the current
-//    GEMM's fragment, each refilled with the next GEMM's half once consumed.
+// Register double buffer for a sequence of 128-deep chunk GEMMs of 32- and
+// 64-row tiles (two workgroups per CU) whose weight operands are known in
+// advance: the two halves of the current GEMM's fragment, each refilled with
+// the next GEMM's half once consumed, so the loads' L2 latency overlaps the MFMA
+// work (and the barriers) in between instead of stalling every k-group.
 template <int M, int W = 4>
 struct WStream {
-    static constexpr int NGF = kEmbed / Shape<M, W>::KG;  // k-groups of one 128-deep GEMM
-    static constexpr bool WHOLE = M == 16;
-    static constexpr int NG = WHOLE ? NGF : NGF / 2;
+    static_assert(Shape<M, W>::MT == 32, "32x32x2 tiles");
+    static constexpr int NG = kEmbed / Shape<M, W>::KG / 2;  // k-groups per half
     BFrag<M, W, NG> b[2];
     int total;  // GEMMs in the sequence
 
@@ -226,84 +206,43 @@ struct WStream {
     __device__ __forceinline__ void start(int n, Src src) {
         total = n;
         const FragSrc f0 = src(0);
-        if constexpr (WHOLE) {
-            const FragSrc f1 = src(1);
-            load_frag_t<M, W, NG>(b[0], f0.p, f0.ld, 0);
-            load_frag_t<M, W, NG>(b[1], f1.p, f1.ld, 0);
-        } else {
-            load_frag_t<M, W, NG>(b[0], f0.p, f0.ld, 0);
-            load_frag_t<M, W, NG>(b[1], f0.p, f0.ld, NG);
-        }
+        load_frag<M, W, NG>(b[0], f0, 0);
+        load_frag<M, W, NG>(b[1], f0, NG);
     }
 
-    // acc += A @ W_s for the s-th GEMM of the sequence (ROLE = s & 1), then
-    // refills the consumed registers.
+    // acc += A @ W_s for the s-th GEMM of the sequence, then refills the
+    // consumed registers with the next GEMM's operand.
     template <int ROLE, class Src>
     __device__ __forceinline__ void gemm(AccTile<M, W>& acc, const float* a_lds, int s, Src src) {
-        if constexpr (WHOLE) {
-            const FragSrc f = src(s + 2 < total ? s + 2 : s);
-            gemm_frag_refill<M, W, NG>(acc, a_lds, b[ROLE], f.p, f.ld, 0);
-        } else {
-            const bool more = s + 1 < total;
-            FragSrc f{nullptr, 0};
-            if (more) f = src(s + 1);
-            gemm_frag<M, W, NG>(acc, a_lds, b[0], 0);
-            if (more) load_frag_t<M, W, NG>(b[0], f.p, f.ld, 0);
-            gemm_frag<M, W, NG>(acc, a_lds, b[1], NG);
-            if (more) load_frag_t<M, W, NG>(b[1], f.p, f.ld, NG);
-        }
+        const bool more = s + 1 < total;
+        FragSrc f{nullptr, 0};
+        if (more) f = src(s + 1);
+        gemm_frag<M, W, NG>(acc, a_lds, b[0], 0);
+        if (more) load_frag<M, W, NG>(b[0], f, 0);
+        gemm_frag<M, W, NG>(acc, a_lds, b[1], NG);
+        if (more) load_frag<M, W, NG>(b[1], f, NG);
     }
 };
 
-// Offset of element (n, k) of a matrix read as rows n of contraction length K
-// (K a multiple of 128) in the fragment-tiled layout of frag_fwd / frag_bwd:
-// 16 x 128 tiles, tile (n / 16, k / 128) at (n / 16) 16 K + (k / 128) 2048, and
-// inside a tile the float4 of lane q 16 + n % 16 for k-group g = k % 128 / 16 at
-// g 256 + (q 16 + n % 16) 4, q = k % 16 / 4. One k-group of one 16-row strip
-// is then 64 consecutive float4s in the lane order of a 16x16x4 B operand.
-__host__ __device__ constexpr uint32_t frag_index(uint32_t n, uint32_t k, uint32_t K) {
-    return (n >> 4) * 16u * K + (k >> 7) * 2048u + ((k & 127u) >> 4) * 256u + ((k & 15u) >> 2) * 64u +
-           (n & 15u) * 4u + (k & 3u);
-}
-
-// Weight stream for 16-row tiles over the fragment-tiled copies: a GEMM's
-// operand for one wave is one 16 x 128 tile per 16 output columns, and each
-// k-group is one float4 per lane from 1 KB of consecutive memory (eight whole
-// cache lines), loaded straight into the MFMA registers. Two whole fragments,
+// Weight stream for 16-row tiles (registers to spare): two whole fragments,
 // one per GEMM role, each refilled two GEMMs ahead one k-group at a time right
-// after that k-group's MFMAs; past the end of the sequence a GEMM reloads its
-// own operand, so every path issues the same loads. A FragSrc here points at
-// the tile of the chunk's first output column and ld is the matrix's
-// contraction length K (16-row strips are 16 K floats apart).
+// after that k-group's MFMAs, so a wave's loads leave one at a time over the
+// GEMM instead of as a burst after it. Past the end of the sequence a GEMM
+// reloads its own operand: every path issues the same loads, so the compiler's
+// vector-memory wait counts stay exact at the chunk loop's head.
 template <int M, int W>
 struct TStream {
     using S = Shape<M, W>;
-    static_assert(S::MT == 16 && S::KG == 16, "16x16x4 tiles");
+    static_assert(S::MT == 16, "16x16x4 tiles");
     static constexpr int NGF = kEmbed / S::KG;  // k-groups of one 128-deep GEMM
     BFrag<M, W, NGF> b[2];
     int total;
 
-    static __device__ __forceinline__ const float* lane_ptr(const FragSrc& f, int ct) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        return f.p + (size_t)(wave * S::CT + ct) * 16 * f.ld + 4 * lane;
-    }
-    static __device__ __forceinline__ void load_group(BFrag<M, W, NGF>& f, const FragSrc& src, int g) {
-#pragma unroll
-        for (int ct = 0; ct < S::CT; ++ct) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(lane_ptr(src, ct) + 256 * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
-        }
-    }
-
     template <class Src>
     __device__ __forceinline__ void start(int n, Src src) {
         total = n;
-        const FragSrc f0 = src(0), f1 = src(1);
-#pragma unroll
-        for (int g = 0; g < NGF; ++g) load_group(b[0], f0, g);
-#pragma unroll
-        for (int g = 0; g < NGF; ++g) load_group(b[1], f1, g);
+        load_frag<M, W, NGF>(b[0], src(0), 0);
+        load_frag<M, W, NGF>(b[1], src(1), 0);
     }
 
     template <int ROLE, class Src>
@@ -326,7 +265,14 @@ struct TStream {
 #pragma unroll
                     for (int ct = 0; ct < S::CT; ++ct)
                         acc[rt][ct] = S::mfma(a[g][rt][j], b[ROLE].b[g][ct][j], acc[rt][ct]);
-            load_group(b[ROLE], f, g);
+#pragma unroll
+            for (int ct = 0; ct < S::CT; ++ct) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(frag_lane<M, W>(f, ct) + 256 * g);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[ROLE].b[g][ct][j] = v[j];
+            }
+            // keep the interleave: the scheduler would otherwise sink every
+            // load to the end of the GEMM to shorten their live ranges
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -423,28 +369,19 @@ __device__ __forceinline__ void fwd_layernorm(FwdSmem<M, NV>& sm, const FwdRegs<
 
 // The forward's GEMM sequence: for block l and chunk c, GEMM 2 (l NC + c)
 // is V_c = xs Up[:, c] (weights Up^T rows c, [H][128]) and the next one is
-// h += V_c Down[c, :] (weights Down^T columns c, [128][H]); both from the
-// transposed copies in params_t.
+// h += V_c Down[c, :] (weights Down^T columns c, [128][H]), read from the
+// fragment-tiled transposed copies for MT x MT tiles (frag_fwd32 or
+// frag_fwd16): Up^T's chunk c (K = 128) starts at row 128 c, Down^T's chunk c
+// (K = H) at tile column c.
+template <int MT>
 struct FwdSeq {
     const mg_policy_view* pv;
     int nc;
     __device__ __forceinline__ FragSrc operator()(int s) const {
         const int l = s / (2 * nc), c = (s >> 1) % nc;
-        if ((s & 1) == 0) return {pv->params_t + pv->off_up[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
-        return {pv->params_t + pv->off_down[l] + kChunk * c, pv->hidden};
-    }
-};
-
-// The same sequence over the fragment-tiled copies in frag_fwd (for TStream):
-// Up^T rows c (K = 128) start at tile row 128 c / 16, Down^T's chunk c (K = H)
-// at tile column c.
-struct FwdSeqF {
-    const mg_policy_view* pv;
-    int nc;
-    __device__ __forceinline__ FragSrc operator()(int s) const {
-        const int l = s / (2 * nc), c = (s >> 1) % nc;
-        if ((s & 1) == 0) return {pv->frag_fwd + pv->off_up[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
-        return {pv->frag_fwd + pv->off_down[l] + 16 * kChunk * c, pv->hidden};
+        const float* base = MT == 32 ? pv->frag_fwd32 : pv->frag_fwd16;
+        if ((s & 1) == 0) return {base + pv->off_up[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
+        return {base + pv->off_down[l] + MT * kChunk * c, pv->hidden};
     }
 };
 
@@ -455,12 +392,11 @@ struct FwdSeqF {
 // whose first 2 L NC GEMMs are the forward's (FwdSeq, or a longer sequence
 // that continues past the forward). With VOUT the relu'd hidden activations
 // are also written to v_out ([M][hidden], row-major).
-template <int M, int W = 4, bool VOUT = false, int NV = 1, class Seq = FwdSeq, class Stream = WStream<M, W>>
+template <int M, int W, bool VOUT, int NV, class Seq, class Stream>
 __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSmem<M, NV>& sm, FwdRegs<M, W>& R,
-                                          Stream& ws, float* v_out = nullptr, Seq seq = Seq{}) {
+                                          Stream& ws, float* v_out, Seq seq) {
     using S = Shape<M, W>;
     const int H = (int)pv.hidden, NC = H / kChunk;
-    if constexpr (std::is_same<Seq, FwdSeq>::value || std::is_same<Seq, FwdSeqF>::value) seq = Seq{&pv, NC};
     for (int c = 0; c < NC; ++c) {
         const int s = 2 * (l * NC + c);
         float* vs = sm.vs[NV == 2 ? (c & 1) : 0];
@@ -498,14 +434,13 @@ __device__ __forceinline__ void fwd_head(const float* Wh, FwdSmem<M, NV>& sm, fl
 }
 
 // Whole forward: obs staged in obsL ([M][O], LDS) -> head in headL ([M][HD], LDS).
-// 16-row tiles read the fragment-tiled copies (TStream); taller tiles stream
-// half-fragments of the transposed copies (WStream).
+// 16-row tiles stream whole fragments (TStream), taller tiles half-fragments
+// (WStream).
 template <int M, int W = 4>
 __device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem<M>& sm, FwdRegs<M, W>& R,
                                                const float* obsL, int O, float* headL, int HD) {
-    constexpr bool TILED = M == 16;
-    using Stream = typename std::conditional<TILED, TStream<M, W>, WStream<M, W>>::type;
-    using Seq = typename std::conditional<TILED, FwdSeqF, FwdSeq>::type;
+    using Stream = typename std::conditional<M == 16, TStream<M, W>, WStream<M, W>>::type;
+    using Seq = FwdSeq<Shape<M, W>::MT>;
     const int NC = (int)pv.hidden / kChunk;
     const Seq seq{&pv, NC};
     Stream ws;

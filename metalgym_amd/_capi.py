@@ -31,7 +31,7 @@ class EnvDesc(C.Structure):
 
 
 class PolicyView(C.Structure):
-    _fields_ = [("params", P), ("params_t", P), ("frag_fwd", P), ("frag_bwd", P)] + [(n, u32) for n in ("obs_dim", "act_dim", "embed", "hidden", "layers", "head_dim",
+    _fields_ = [("params", P), ("frag_fwd32", P), ("frag_fwd16", P), ("frag_bwd16", P)] + [(n, u32) for n in ("obs_dim", "act_dim", "embed", "hidden", "layers", "head_dim",
                                                        "continuous", "count", "off_in_w", "off_in_b")] + [
         ("off_ln_gamma", u32 * (MAX_LAYERS + 1)),
         ("off_ln_beta", u32 * (MAX_LAYERS + 1)),

@@ -46,11 +46,11 @@ struct TrainStep {
     float beta1_pow, beta2_pow;
 };
 
-// params_t (the transposed block matrices) and the fragment-tiled copies
-// (frag_fwd, frag_bwd) from params.
-int launch_transpose_blocks(hipStream_t st, const mg_policy_view& pv);
+// The fragment-tiled copies of the block matrices (frag_fwd32, frag_fwd16,
+// frag_bwd16) from params.
+int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv);
 // MG_OK if the block matrices sit contiguously from float_group (the layout
-// the Adam and transpose kernels tile).
+// the Adam and derive kernels tile).
 int check_matrix_layout(const mg_policy_view& pv);
 
 int train_ws_bytes(const mg_policy_view& pv, uint32_t rows, size_t* bytes);

@@ -257,9 +257,9 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
     int rc;
     if ((rc = check_matrix_layout(pv))) return fail(rc);
     if ((rc = device_alloc((void**)&pv.params, (size_t)pv.count * 4, "PPOModel params")) ||
-        (rc = device_alloc((void**)&pv.params_t, (size_t)pv.count * 4, "PPOModel transposed matrices")) ||
-        (rc = device_alloc((void**)&pv.frag_fwd, (size_t)pv.count * 4, "PPOModel forward matrix tiles")) ||
-        (rc = device_alloc((void**)&pv.frag_bwd, (size_t)pv.count * 4, "PPOModel backward matrix tiles")) ||
+        (rc = device_alloc((void**)&pv.frag_fwd32, (size_t)pv.count * 4, "PPOModel forward matrix tiles")) ||
+        (rc = device_alloc((void**)&pv.frag_fwd16, (size_t)pv.count * 4, "PPOModel forward matrix tiles")) ||
+        (rc = device_alloc((void**)&pv.frag_bwd16, (size_t)pv.count * 4, "PPOModel backward matrix tiles")) ||
         (rc = device_alloc((void**)&p->m, (size_t)pv.count * 4, "PPOModel adam m")) ||
         (rc = device_alloc((void**)&p->v, (size_t)pv.count * 4, "PPOModel adam v")) ||
         (rc = device_alloc((void**)&p->obs_slots, (T + 1) * n * env->obs_dim * 4, "obs slots")) ||
@@ -288,11 +288,11 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
         hipMemsetAsync(p->adv, 0, slot * 4, st) != hipSuccess ||
         hipMemsetAsync(p->ret, 0, slot * 4, st) != hipSuccess ||
         hipMemsetAsync(p->head, 0, (size_t)p->head_cap * pv.head_dim * 4, st) != hipSuccess ||
-        hipMemsetAsync(pv.params_t, 0, (size_t)pv.count * 4, st) != hipSuccess ||
-        hipMemsetAsync(pv.frag_fwd, 0, (size_t)pv.count * 4, st) != hipSuccess ||
-        hipMemsetAsync(pv.frag_bwd, 0, (size_t)pv.count * 4, st) != hipSuccess)
+        hipMemsetAsync(pv.frag_fwd32, 0, (size_t)pv.count * 4, st) != hipSuccess ||
+        hipMemsetAsync(pv.frag_fwd16, 0, (size_t)pv.count * 4, st) != hipSuccess ||
+        hipMemsetAsync(pv.frag_bwd16, 0, (size_t)pv.count * 4, st) != hipSuccess)
         return fail(set_error(MG_ERR_HIP, "PPOModel: initialisation upload failed"));
-    if ((rc = launch_transpose_blocks(st, pv))) return fail(rc);
+    if ((rc = launch_derive_blocks(st, pv))) return fail(rc);
     if (hipStreamSynchronize(st) != hipSuccess)
         return fail(set_error(MG_ERR_HIP, "PPOModel: initialisation upload failed"));
     p->order.resize(p->blocks);
@@ -306,9 +306,9 @@ int mg_ppo_destroy(mg_ppo* p) {
     if (!p) return MG_OK;
     if (p->gym && p->gym->stream) (void)hipStreamSynchronize(p->gym->stream);
     (void)hipFree(p->pv.params);
-    (void)hipFree(p->pv.params_t);
-    (void)hipFree(p->pv.frag_fwd);
-    (void)hipFree(p->pv.frag_bwd);
+    (void)hipFree(p->pv.frag_fwd32);
+    (void)hipFree(p->pv.frag_fwd16);
+    (void)hipFree(p->pv.frag_bwd16);
     (void)hipFree(p->m);
     (void)hipFree(p->v);
     (void)hipFree(p->obs_slots);
@@ -486,7 +486,7 @@ int mg_ppo_set_params(mg_ppo* p, const float* host, uint32_t count) {
 
 int mg_ppo_params_updated(mg_ppo* p) {
     MG_CHECK(p, MG_ERR_INVALID, "params_updated: null model");
-    int rc = launch_transpose_blocks(p->gym->stream, p->pv);
+    int rc = launch_derive_blocks(p->gym->stream, p->pv);
     if (rc) return rc;
     MG_HIP(hipStreamSynchronize(p->gym->stream), "params_updated synchronize");
     return MG_OK;

@@ -136,15 +136,15 @@ __device__ __forceinline__ void bwd_layernorm(TSmem& sm, TRegs& G, const float* 
 // GEMM 2 ((L - 1 - l) NC + c) is dV_c = dh Down[c, :]^T (weights Down rows c,
 // [128 hidden][128]) and the next one is dx += dV_c Up[:, c]^T (weights Up
 // columns c, [128][H]), both from the fragment-tiled copies of the matrices as
-// stored (frag_bwd): Down rows c (K = 128) start at tile row 128 c / 16, Up's
+// stored (frag_bwd16): Down rows c (K = 128) start at tile row 128 c / 16, Up's
 // chunk c (K = H) at tile column c.
 struct BwdSeq {
     const mg_policy_view* pv;
     int nc;
     __device__ __forceinline__ FragSrc operator()(int s) const {
         const int l = (int)pv->layers - 1 - s / (2 * nc), c = (s >> 1) % nc;
-        if ((s & 1) == 0) return {pv->frag_bwd + pv->off_down[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
-        return {pv->frag_bwd + pv->off_up[l] + 16 * kChunk * c, pv->hidden};
+        if ((s & 1) == 0) return {pv->frag_bwd16 + pv->off_down[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
+        return {pv->frag_bwd16 + pv->off_up[l] + 16 * kChunk * c, pv->hidden};
     }
 };
 
@@ -156,7 +156,7 @@ struct TrainSeq {
     int nc;
     __device__ __forceinline__ FragSrc operator()(int s) const {
         const int F = 2 * (int)pv->layers * nc;
-        return s < F ? FwdSeqF{pv, nc}(s) : BwdSeq{pv, nc}(s - F);
+        return s < F ? FwdSeq<16>{pv, nc}(s) : BwdSeq{pv, nc}(s - F);
     }
 };
 
@@ -553,7 +553,7 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
 // The block matrices are contiguous from float_group: per block up [128 x H]
 // then down [H x 128]. Both matrix kinds split into (128 x H) / 1024 tiles of
 // 32 x 32; tile t's matrix, its row/column extents and the tile's origin.
-constexpr int kTT = 32;  // transpose tile edge
+constexpr int kTT = 32;  // block-matrix tile edge of the Adam and derive kernels
 struct MatTile {
     uint32_t base;  // arena offset of the matrix
     uint32_t rows, cols;
@@ -570,29 +570,24 @@ __device__ __forceinline__ MatTile mat_tile(uint32_t t, uint32_t float_group, ui
     m.c0 = (tt % (m.cols / kTT)) * kTT;
     return m;
 }
-constexpr int kTileLd = kTT + 1;  // LDS row stride of a transpose tile
-
-// Writes the tile held in lds ([r][c], stride kTileLd) transposed into
-// param_t: element (r0 + r, c0 + c) goes to base + (c0 + c) * rows + r0 + r.
-// Coalesced along r. Starts with a barrier.
-__device__ __forceinline__ void store_tile_t(const MatTile& m, const float* lds, float* param_t) {
-    __syncthreads();
-    const int t = threadIdx.x, r = t & (kTT - 1);
-#pragma unroll
-    for (int e = 0; e < kTT * kTT / 256; ++e) {
-        const int c = (256 / kTT) * e + t / kTT;
-        param_t[m.base + (size_t)(m.c0 + c) * m.rows + m.r0 + r] = lds[r * kTileLd + c];
-    }
-}
+constexpr int kTileLd = kTT + 1;  // LDS row stride of such a tile
 
 // Writes the tile held in lds ([r][c], stride kTileLd) to the fragment-tiled
-// copies: frag_bwd reads the matrix as stored (rows n = r, contraction k = c,
-// K = cols), frag_fwd its transpose (n = c, k = r, K = rows). Each thread writes
-// one float4 (four consecutive k of one n) to each; a wave's 64 float4s are
-// one 1 KB run. No barrier (the caller has ordered the LDS writes).
-__device__ __forceinline__ void store_tile_frag(const MatTile& m, const float* lds, float* frag_fwd,
-                                                float* frag_bwd) {
+// copies: frag_fwd32 and frag_fwd16 read its transpose (rows n = c,
+// contraction k = r, K = rows), frag_bwd16 the matrix as stored (n = r, k = c,
+// K = cols). Each thread writes one float4 (four consecutive k of one n) to
+// each; a wave's 64 float4s form one 1 KB run. Starts with a barrier.
+__device__ __forceinline__ void store_tile_frags(const MatTile& m, const float* lds, float* fwd32, float* fwd16,
+                                                 float* bwd16) {
+    __syncthreads();
     const int t = threadIdx.x;
+    {  // 32-wide strips: the tile is one strip's four k-groups, 4 KB in a row
+        const int n = t & 31, k = 8 * (t >> 6) + 4 * ((t >> 5) & 1);
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = lds[(k + j) * kTileLd + n];
+        *reinterpret_cast<f32x4*>(fwd32 + m.base + frag_index<32>(m.c0 + n, m.r0 + k, m.rows)) = v;
+    }
     const int n = 16 * (t >> 7) + (t & 15), k = 16 * ((t >> 6) & 1) + 4 * ((t >> 4) & 3);
     f32x4 vb, vf;
 #pragma unroll
@@ -600,15 +595,14 @@ __device__ __forceinline__ void store_tile_frag(const MatTile& m, const float* l
         vb[j] = lds[n * kTileLd + k + j];
         vf[j] = lds[(k + j) * kTileLd + n];
     }
-    *reinterpret_cast<f32x4*>(frag_bwd + m.base + frag_index(m.r0 + n, m.c0 + k, m.cols)) = vb;
-    *reinterpret_cast<f32x4*>(frag_fwd + m.base + frag_index(m.c0 + n, m.r0 + k, m.rows)) = vf;
+    *reinterpret_cast<f32x4*>(bwd16 + m.base + frag_index<16>(m.r0 + n, m.c0 + k, m.cols)) = vb;
+    *reinterpret_cast<f32x4*>(fwd16 + m.base + frag_index<16>(m.c0 + n, m.r0 + k, m.rows)) = vf;
 }
 
-// params_t and the fragment-tiled copies from params, one tile per workgroup.
-__global__ void __launch_bounds__(256) transpose_blocks_kernel(const float* __restrict__ param,
-                                                               float* __restrict__ param_t, float* __restrict__ frag_fwd,
-                                                               float* __restrict__ frag_bwd, uint32_t float_group,
-                                                               uint32_t H) {
+// The fragment-tiled copies from params, one tile per workgroup.
+__global__ void __launch_bounds__(256) derive_blocks_kernel(const float* __restrict__ param, float* __restrict__ fwd32,
+                                                            float* __restrict__ fwd16, float* __restrict__ bwd16,
+                                                            uint32_t float_group, uint32_t H) {
     __shared__ float lds[kTT * kTileLd];
     const MatTile m = mat_tile(blockIdx.x, float_group, H);
     const int t = threadIdx.x, c = t & (kTT - 1);
@@ -617,15 +611,14 @@ __global__ void __launch_bounds__(256) transpose_blocks_kernel(const float* __re
         const int r = (256 / kTT) * e + t / kTT;
         lds[r * kTileLd + c] = param[m.base + (size_t)(m.r0 + r) * m.cols + m.c0 + c];
     }
-    store_tile_t(m, lds, param_t);
-    store_tile_frag(m, lds, frag_fwd, frag_bwd);
+    store_tile_frags(m, lds, fwd32, fwd16, bwd16);
 }
 
 struct AdamArgs {
     float* param;
-    float* param_t;
-    float* frag_fwd;
-    float* frag_bwd;
+    float* frag_fwd32;
+    float* frag_fwd16;
+    float* frag_bwd16;
     const float* grad;
     float* mom;
     float* var;
@@ -673,9 +666,8 @@ __device__ __forceinline__ float adam_clip_scale(const AdamArgs& a) {
 }
 
 // Workgroups [0, mat_tiles) update one 32 x 32 block-matrix tile each and
-// write it to param_t and the fragment-tiled copies as well; the rest update
-// the vector group and the head elementwise. Workgroup 0 also records the
-// pre-clip norm.
+// write it to the fragment-tiled copies as well; the rest update the vector
+// group and the head elementwise. Workgroup 0 also records the pre-clip norm.
 __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
     __shared__ float lds[kTT * kTileLd];
     constexpr int PER = kTT * kTT / 256;  // tile elements per thread
@@ -697,8 +689,7 @@ __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
             const int r = (256 / kTT) * e + t / kTT;
             lds[r * kTileLd + c] = adam_elem(a, idx[e], in[e], scale);
         }
-        store_tile_t(m, lds, a.param_t);
-        store_tile_frag(m, lds, a.frag_fwd, a.frag_bwd);
+        store_tile_frags(m, lds, a.frag_fwd32, a.frag_fwd16, a.frag_bwd16);
         return;
     }
     const uint32_t j = (blockIdx.x - a.mat_tiles) * 256 + t;
@@ -777,12 +768,12 @@ int check_matrix_layout(const mg_policy_view& pv) {
     return MG_OK;
 }
 
-int launch_transpose_blocks(hipStream_t st, const mg_policy_view& pv) {
+int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv) {
     int rc = check_matrix_layout(pv);
     if (rc) return rc;
-    hipLaunchKernelGGL(dev::transpose_blocks_kernel, dim3(mat_tiles(pv)), dim3(256), 0, st, pv.params, pv.params_t,
-                       pv.frag_fwd, pv.frag_bwd, pv.float_group, pv.hidden);
-    MG_HIP(hipGetLastError(), "transpose launch");
+    hipLaunchKernelGGL(dev::derive_blocks_kernel, dim3(mat_tiles(pv)), dim3(256), 0, st, pv.params, pv.frag_fwd32,
+                       pv.frag_fwd16, pv.frag_bwd16, pv.float_group, pv.hidden);
+    MG_HIP(hipGetLastError(), "derive blocks launch");
     return MG_OK;
 }
 
@@ -867,9 +858,9 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         TimedLaunch tl(MG_K_ADAM, st);
         dev::AdamArgs aa;
         aa.param = pv.params;
-        aa.param_t = pv.params_t;
-        aa.frag_fwd = pv.frag_fwd;
-        aa.frag_bwd = pv.frag_bwd;
+        aa.frag_fwd32 = pv.frag_fwd32;
+        aa.frag_fwd16 = pv.frag_fwd16;
+        aa.frag_bwd16 = pv.frag_bwd16;
         aa.grad = ws.grad;
         aa.mom = m;
         aa.var = v;
