@@ -288,16 +288,16 @@ __device__ __forceinline__ void store_tile(const AccTile<M, W>& acc, float* lds)
     });
 }
 
-// Copies an LDS tile ([M][128], row stride kLds) to global memory
-// (global[row * ld + col]) as float4 rows, NT threads.
-template <int M, int NT>
-__device__ __forceinline__ void copy_rows_g(const float* lds, float* global, size_t ld) {
-#pragma unroll
-    for (int i = threadIdx.x; i < M * kEmbed / 4; i += NT) {
-        const int row = i / (kEmbed / 4), c4 = 4 * (i % (kEmbed / 4));
-        *reinterpret_cast<f32x4*>(global + (size_t)row * ld + c4) =
-            *reinterpret_cast<const f32x4*>(lds + row * kLds + c4);
-    }
+// Writes a register tile to global memory (global[row * ld + col]),
+// optionally through relu. Issued before a barrier, the stores leave while
+// the wave would otherwise wait.
+template <int M, int W = 4, bool RELU = false>
+__device__ __forceinline__ void store_tile_g(const AccTile<M, W>& acc, float* global, size_t ld) {
+    for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
+        float x = acc[rt][ct][r];
+        if (RELU) x = x > 0.0f ? x : 0.0f;
+        global[(size_t)row * ld + col] = x;
+    });
 }
 
 // model/input.metal:11-27: h = b_in + sum_k obs[k] W_in[k], in k order.
@@ -403,10 +403,10 @@ __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSm
         typename S::Acc v[S::RT][S::CT];
         zero<M, W>(v);
         ws.template gemm<0>(v, sm.xs, s, seq);
+        if constexpr (VOUT) store_tile_g<M, W, true>(v, v_out + kChunk * c, H);
         if constexpr (NV == 1) __syncthreads();  // every wave is done reading the previous chunk from vs
         store_tile<M, W, true>(v, vs);
         __syncthreads();
-        if constexpr (VOUT) copy_rows_g<M, S::NT>(vs, v_out + kChunk * c, H);
         ws.template gemm<1>(R.h, vs, s + 1, seq);
     }
 }

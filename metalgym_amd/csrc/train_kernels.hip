@@ -171,9 +171,9 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem
                                           float* tp, float* scratch) {
     const int H = (int)pv.hidden, NC = H / kChunk, F = 2 * (int)pv.layers * NC;
     const TrainSeq seq{&pv, NC};
+    store_tile_g<kTR, kTW>(D.h, dh_store, kEmbed);
     store_tile<kTR, kTW>(D.h, sm.xs);
     __syncthreads();
-    copy_rows_g<kTR, kTNT>(sm.xs, dh_store, kEmbed);
     TRegs G;
     zero<kTR, kTW>(G.h);
     for (int c = 0; c < NC; ++c) {
@@ -189,10 +189,11 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem
         zero<kTR, kTW>(v);
         ws.template gemm<0>(v, sm.xs, s, seq);
         for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-            vs[row * kLds + col] = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
+            const float g = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
+            dv_store[(size_t)row * H + kChunk * c + col] = g;
+            vs[row * kLds + col] = g;
         });
         __syncthreads();
-        copy_rows_g<kTR, kTNT>(vs, dv_store + kChunk * c, H);
         ws.template gemm<1>(G.h, vs, s + 1, seq);
     }
     __syncthreads();

@@ -101,9 +101,16 @@ def test_collect_full_size_subset(mg, orc):
     assert np.isfinite(s["value"]).all() and np.isfinite(s["logp"]).all()
 
 
-@pytest.mark.parametrize("layers,scale", [(1, 1), (3, 2)])
-def test_collect_other_shapes(mg, orc, layers, scale):
-    run_collect_parity(mg, orc, "cartpole", 1024, 4, layers=layers, scale=scale, seed=11, collects=1)
+@pytest.mark.parametrize("n,T,layers,scale", [
+    (1024, 4, 1, 1),
+    (1024, 4, 3, 2),
+    (1024, 2, 8, 1),     # the most blocks (MG_MAX_LAYERS), 16-row tiles
+    (1024, 2, 2, 8),     # the widest hidden layer (1024), 16-row tiles
+    (8192, 2, 2, 8),     # 32-row tiles
+    (32768, 2, 8, 1),    # 64-row tiles
+])
+def test_collect_other_shapes(mg, orc, n, T, layers, scale):
+    run_collect_parity(mg, orc, "cartpole", n, T, layers=layers, scale=scale, seed=11, collects=1)
 
 
 @pytest.mark.parametrize("env", ["cartpole", "voxelnav16", "cartpole_continuous"])

@@ -86,7 +86,9 @@ def float64_moment(pv, params, rows, hp):
     ("cartpole_continuous", 2048, 2, 1024, 2, 2, 4),
     ("voxelnav16", 1024, 2, 512, 1, 2, 4),
     ("cartpole", 1024, 2, 512, 2, 3, 2),      # hidden 256, three blocks
-    ("cartpole", 1024, 2, 512, 1, 5, 2),      # five blocks: the row pass's register-streamed size class
+    ("cartpole", 1024, 2, 512, 1, 5, 2),      # five blocks
+    ("cartpole", 1024, 2, 512, 0, 8, 1),      # the most blocks (MG_MAX_LAYERS), hidden 128
+    ("cartpole", 1024, 2, 512, 1, 2, 8),      # the widest hidden layer (scale 8: 1024)
 ])
 def test_one_minibatch(mg, orc, env, n, T, B, block, layers, scale):
     gym, model, d = setup(mg, orc, env, n, T, B, layers=layers, scale=scale)
