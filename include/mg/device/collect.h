@@ -18,14 +18,16 @@ namespace mg {
 namespace dev {
 
 // Launch shape per tile height: 64- and 32-row tiles run 4 waves and two
-// workgroups per CU; 16-row tiles (runs of at most 512 workgroups, one per CU)
-// of envs with up to 16 observation floats run 8 waves, 16 output columns each
-// (a wider observation held by the env lane would not fit the register budget
-// of 8 waves).
+// workgroups per CU (one when the env lane holds more than 32 observation
+// floats, which do not fit beside the weights at two); 16-row tiles (runs of
+// at most 512 workgroups, one per CU) of envs with up to 16 observation floats
+// run 8 waves, 16 output columns each (a wider observation held by the env
+// lane would not fit the register budget of 8 waves).
 template <int M, int O>
 struct CollectShape {
     static constexpr int W = M == 16 && O <= 16 ? 8 : 4;
     static constexpr int NT = 64 * W;
+    static constexpr int MIN_WG = M == 16 || O > 32 ? 1 : 2;  // workgroups per CU
 };
 
 template <int M, int O, int HD>
@@ -36,7 +38,7 @@ struct CollectSmem {
 };
 
 template <typename Env, int M>
-__global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (M == 16 ? 1 : 2))
+__global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectShape<M, Env::OBS_DIM>::MIN_WG))
     collect_kernel(const mg_collect_args a) {
     using Tr = EnvTraits<Env>;
     using State = typename Env::State;

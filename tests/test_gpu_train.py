@@ -45,13 +45,53 @@ def group_errors(pv, a, b):
     return out
 
 
-def compare_moments(pv, m_gpu, m_orc, what):
-    """The first Adam moment is 0.1 x the clipped gradient. fp32 sums in a
-    different order differ by 1e-6 near the head and up to ~1e-4 in the first
-    block (LayerNorm backward cancels most of its input); a wrong term is O(1)."""
-    errs = group_errors(pv, m_gpu, m_orc)
-    worst = max(errs, key=errs.get)
-    assert errs[worst] < 1e-3, f"{what}: relative L2 error {errs[worst]:.3g} in {worst}; all: {errs}"
+def relu_flip_units(pv, m_gpu, m_orc):
+    """A hidden pre-activation within ~1e-6 of zero can fall on either side of
+    the ReLU under a different fp32 summation order; that unit's gradient path
+    then switches on or off for that row. Its signature: one hidden column of an
+    up matrix holds almost all of that matrix's difference, and the difference
+    spreads from there into the layers below (never into the blocks above or
+    the head). Returns the blocks showing it."""
+    flips = []
+    for l in range(pv.layers):
+        o, c = pv.off_up[l], pv.embed * pv.hidden
+        d = (m_gpu[o:o + c].astype(np.float64) - m_orc[o:o + c]).reshape(pv.embed, pv.hidden)
+        col = (d ** 2).sum(0)
+        share = col.max() / max(col.sum(), 1e-300)
+        print(f"up{l}: worst hidden column {col.argmax()} holds {share:.3f} of the squared difference")
+        if share > 0.9:
+            flips.append(l)
+    return flips
+
+
+def check_moment(pv, m_gpu, m_orc, params, rows, hp):
+    """The GPU's first Adam moment against the oracle's (1e-3 relative L2 per
+    parameter group) and both against a float64 gradient: the GPU must be as
+    close to float64 as the oracle is. Where the ReLU-flip signature explains a
+    difference, the groups it reaches (the flipped block's up matrix and
+    everything below it) are held to the float64 reference at 1e-2 instead, and
+    every group above it stays at the strict bar."""
+    m64 = float64_moment(pv, params, rows, hp)
+    e_pair, e_gpu, e_orc = group_errors(pv, m_gpu, m_orc), group_errors(pv, m_gpu, m64), group_errors(pv, m_orc, m64)
+    print("gpu vs oracle:", e_pair)
+    print("float64 error per group, gpu:", e_gpu, "oracle:", e_orc)
+    flips = relu_flip_units(pv, m_gpu, m_orc) if max(e_pair.values()) >= 1e-3 else []
+    top = max(flips) if flips else -1  # the highest flipped block
+
+    def below(k):  # groups the flip of block `top` reaches
+        if k.startswith(("in_", "ln0")):
+            return top >= 0
+        for l in range(pv.layers):
+            if k in (f"up{l}", f"down{l}", f"ln{l + 1}_gamma", f"ln{l + 1}_beta"):
+                return (l < top) or (k == f"up{l}" and l == top) or (k.startswith("ln") and l + 1 <= top)
+        return False
+
+    for k in e_gpu:
+        if below(k):
+            assert e_gpu[k] < 1e-2, (k, e_gpu[k])
+        else:
+            assert e_pair[k] < 1e-3, (k, e_pair[k])
+            assert e_gpu[k] <= 4 * e_orc[k] + 2e-5, (k, e_gpu[k], e_orc[k])
 
 
 def float64_moment(pv, params, rows, hp):
@@ -102,28 +142,7 @@ def test_one_minibatch(mg, orc, env, n, T, B, block, layers, scale):
     P, M, V = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
     st, grad, head = orc.train_minibatch(d, hp, P, M, V, 1, *block_rows(s, n, B, block), threads=THREADS)
     assert_close(model.head(), head, TOL_HEAD, "recomputed head")
-    compare_moments(model.pv, m1, M, "first moment (clipped gradient)")
-    # both fp32 gradients against the float64 one: the GPU is as close as the oracle
-    m64 = float64_moment(model.pv, p0, block_rows(s, n, B, block), hp)
-    e_gpu, e_orc = group_errors(model.pv, m1, m64), group_errors(model.pv, M, m64)
-    print("float64 gradient error per group, gpu:", e_gpu, "oracle:", e_orc)
-    # A hidden pre-activation within ~1e-6 of zero can fall on either side of the
-    # ReLU under a different fp32 summation order; that unit's gradient path then
-    # switches on or off. Its signature: one column of an up matrix holds almost
-    # all of that matrix's error (the error then spreads into the layers below).
-    pv = model.pv
-    flip = False
-    for l in range(pv.layers):
-        o = pv.off_up[l]
-        d = (m1[o:o + pv.embed * pv.hidden] - m64[o:o + pv.embed * pv.hidden]).reshape(pv.embed, pv.hidden)
-        col = (d.astype(np.float64) ** 2).sum(0)
-        share = col.max() / max(col.sum(), 1e-300)
-        print(f"up{l}: worst hidden column {col.argmax()} holds {share:.3f} of the squared error")
-        flip |= share > 0.9 and e_gpu[f"up{l}"] > 2e-5
-    for k in e_gpu:
-        assert e_gpu[k] < 1e-3, (k, e_gpu[k])
-        if not flip:
-            assert e_gpu[k] <= 4 * e_orc[k] + 2e-5, (k, e_gpu[k], e_orc[k])
+    check_moment(model.pv, m1, M, p0, block_rows(s, n, B, block), hp)
     assert_close(p1, P, TOL_TRAIN, "post-Adam weights")
     got, want = np.array(model.last_stats().as_tuple()), np.array(st.as_tuple())
     assert_close(got[[0, 1, 2, 3, 5]], want[[0, 1, 2, 3, 5]], TOL_TRAIN, "LossStats")
