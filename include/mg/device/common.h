@@ -33,11 +33,26 @@ __device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
 __device__ __forceinline__ int c32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 __device__ __forceinline__ int c16_row(int r, int lane) { return 4 * (lane >> 4) + r; }
 
-// Sum over groups of G consecutive lanes (G a power of two <= 64).
+// v from another lane of its 16-lane row (a DPP move; CTRL is the dpp_ctrl
+// pattern).
+template <int CTRL>
+__device__ __forceinline__ float dpp_lane(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over groups of G consecutive lanes (G a power of two <= 64); every lane
+// of a group gets the same bits. Inside a 16-lane row the partners come from
+// DPP moves (quad_perm xor 1, xor 2, then the half-row and row mirrors, each
+// pairing the group's halves); wider groups add one lane shuffle per doubling.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, kWave);
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "power-of-two group");
+    if constexpr (G >= 2) v += dpp_lane<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    if constexpr (G >= 4) v += dpp_lane<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    if constexpr (G >= 8) v += dpp_lane<0x141>(v);  // row_half_mirror
+    if constexpr (G >= 16) v += dpp_lane<0x140>(v); // row_mirror
+    if constexpr (G >= 32) v += __shfl_xor(v, 16, kWave);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, kWave);
     return v;
 }
 
