@@ -56,6 +56,19 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Maximum over groups of G consecutive lanes, the same partner pattern.
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "power-of-two group");
+    if constexpr (G >= 2) v = fmaxf(v, dpp_lane<0xB1>(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp_lane<0x4E>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp_lane<0x141>(v));
+    if constexpr (G >= 16) v = fmaxf(v, dpp_lane<0x140>(v));
+    if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, kWave));
+    return v;
+}
+
 // Store OBS_DIM floats with the widest stores the row alignment allows.
 template <int N>
 __device__ __forceinline__ void store_floats(float* dst, const float* src) {

@@ -244,11 +244,12 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
         const int ln = idx / (2 * kEmbed), k = idx % (2 * kEmbed);
         L.ln[idx] = k < kEmbed ? pv.params[pv.off_ln_gamma[ln] + k] : pv.params[pv.off_ln_beta[ln] + k - kEmbed];
     }
-    // the loss inputs of this lane's row
-    float an = 0.0f, oldLp = 0.0f, ret = 0.0f;
+    // the loss inputs of this thread's row (32 threads per row)
+    const int lrow = tid >> 5, lk = tid & 31;
+    float an, oldLp, ret;
     int act = 0;
-    if (tid < M) {
-        const size_t gr = g0 + tid;
+    {
+        const size_t gr = g0 + lrow;
         const float mean = a.adv_stats[2 * a.step.block], inv = a.adv_stats[2 * a.step.block + 1];
         an = (a.adv_slots[gr] - mean) * inv;
         oldLp = a.logp_slots[gr];
@@ -272,71 +273,82 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
                           L.sd + NL * M, ws.x + ((size_t)NL * B + r0) * kEmbed);
     fwd_head<M, kTW>(L.wh, sm, L.head, HD);
 
-    // ---- loss and head gradient, one lane per row ----
-    if (tid < M) {
-        const float* h = L.head + tid * HD;
-        float* dz = L.dhead + tid * HD;
+    // ---- loss and head gradient: 32 threads per row, thread k owning head
+    // columns k and k + 32 (ACT_DIM <= 63), the row sums as group reductions ----
+    static_assert(kTNT == 32 * M && kMaxHeadT <= 64, "32 threads per row, two columns each");
+    {
+        const float* h = L.head + lrow * HD;
+        float* dz = L.dhead + lrow * HD;
         const float scale = 1.0f / (float)B;
         const float clip = a.hp.clip, ec = a.hp.entropy_coef;
-        float entropy = 0.0f, logpA, ratio, gLogp, policyLoss;
+        const int j0 = lk, j1 = lk + 32;
+        const bool v0 = j0 < A, v1 = j1 < A;
+        float entropy, logpA;
+        float d0 = 0.0f, d1 = 0.0f, is0 = 0.0f, is1 = 0.0f, p0 = 0.0f, p1 = 0.0f, lp0 = 0.0f, lp1 = 0.0f;
         if (!pv.continuous) {  // model/policy.metal:14-69
-            float rowMax = -__builtin_huge_valf();
-            for (int j = 0; j < A; ++j) rowMax = rowMax < h[j] ? h[j] : rowMax;
-            float s = 0.0f;
-            for (int j = 0; j < A; ++j) s += mg::expf(h[j] - rowMax);
-            const float lse = rowMax + mg::logf(s);
-            for (int j = 0; j < A; ++j) {
-                const float lp = h[j] - lse;
-                entropy -= mg::expf(lp) * lp;
-            }
+            const float z0 = v0 ? h[j0] : -__builtin_huge_valf(), z1 = v1 ? h[j1] : -__builtin_huge_valf();
+            const float rowMax = group_max<32>(fmaxf(z0, z1));
+            float e = v0 ? mg::expf(z0 - rowMax) : 0.0f;
+            if (v1) e += mg::expf(z1 - rowMax);
+            const float lse = rowMax + mg::logf(group_sum<32>(e));
+            float ent = 0.0f;
+            if (v0) lp0 = z0 - lse, p0 = mg::expf(lp0), ent -= p0 * lp0;
+            if (v1) lp1 = z1 - lse, p1 = mg::expf(lp1), ent -= p1 * lp1;
+            entropy = group_sum<32>(ent);
             logpA = h[act] - lse;
-            ratio = mg::expf(logpA - oldLp);
-            const float surr1 = ratio * an;
-            const float cr = fminf(fmaxf(ratio, 1.0f - clip), 1.0f + clip);
-            const float surr2 = cr * an;
-            policyLoss = -(surr1 < surr2 ? surr1 : surr2);
-            gLogp = (surr1 <= surr2) ? -an * ratio : 0.0f;
-            for (int j = 0; j < A; ++j) {
-                const float lp = h[j] - lse;
-                const float prob = mg::expf(lp);
-                const float g = gLogp * ((j == act ? 1.0f : 0.0f) - prob) + ec * prob * (lp + entropy);
-                dz[j] = g * scale;
-            }
         } else {  // model/gaussian.metal:76-135
-            const float* actg = static_cast<const float*>(a.action_slots) + (g0 + tid) * A;
+            const float* actg = static_cast<const float*>(a.action_slots) + (g0 + lrow) * A;
             const float* logStd = pv.params + pv.off_log_std;
-            float logp = 0.0f;
-            for (int k = 0; k < A; ++k) {
-                const float ls = logStd[k];
-                const float d = (actg[k] - h[k]) * mg::expf(-ls);
-                logp += -0.5f * d * d - ls - kLogSqrt2Pi;
-                entropy += ls + kLogSqrt2Pi + 0.5f;
+            float lp = 0.0f, ent = 0.0f;
+            if (v0) {
+                const float ls = logStd[j0];
+                is0 = mg::expf(-ls);
+                d0 = (actg[j0] - h[j0]) * is0;
+                lp += -0.5f * d0 * d0 - ls - kLogSqrt2Pi;
+                ent += ls + kLogSqrt2Pi + 0.5f;
             }
-            logpA = logp;
-            ratio = mg::expf(logp - oldLp);
-            const float surr1 = ratio * an;
-            const float cr = fminf(fmaxf(ratio, 1.0f - clip), 1.0f + clip);
-            const float surr2 = cr * an;
-            policyLoss = -(surr1 < surr2 ? surr1 : surr2);
-            gLogp = (surr1 <= surr2) ? -an * ratio : 0.0f;
-            for (int k = 0; k < A; ++k) {
-                const float ls = logStd[k];
-                const float invStd = mg::expf(-ls);
-                const float d = (actg[k] - h[k]) * invStd;
-                dz[k] = gLogp * d * invStd * scale;
-                L.dls[tid * A + k] = (gLogp * (d * d - 1.0f) - ec) * scale;
+            if (v1) {
+                const float ls = logStd[j1];
+                is1 = mg::expf(-ls);
+                d1 = (actg[j1] - h[j1]) * is1;
+                lp += -0.5f * d1 * d1 - ls - kLogSqrt2Pi;
+                ent += ls + kLogSqrt2Pi + 0.5f;
+            }
+            logpA = group_sum<32>(lp);
+            entropy = group_sum<32>(ent);
+        }
+        const float ratio = mg::expf(logpA - oldLp);
+        const float surr1 = ratio * an;
+        const float cr = fminf(fmaxf(ratio, 1.0f - clip), 1.0f + clip);
+        const float surr2 = cr * an;
+        const float gLogp = (surr1 <= surr2) ? -an * ratio : 0.0f;
+        if (!pv.continuous) {
+            if (v0) dz[j0] = (gLogp * ((j0 == act ? 1.0f : 0.0f) - p0) + ec * p0 * (lp0 + entropy)) * scale;
+            if (v1) dz[j1] = (gLogp * ((j1 == act ? 1.0f : 0.0f) - p1) + ec * p1 * (lp1 + entropy)) * scale;
+        } else {
+            if (v0) {
+                dz[j0] = gLogp * d0 * is0 * scale;
+                L.dls[lrow * A + j0] = (gLogp * (d0 * d0 - 1.0f) - ec) * scale;
+            }
+            if (v1) {
+                dz[j1] = gLogp * d1 * is1 * scale;
+                L.dls[lrow * A + j1] = (gLogp * (d1 * d1 - 1.0f) - ec) * scale;
             }
         }
-        const float vErr = h[A] - ret;
-        dz[A] = a.hp.value_coef * vErr * scale;
-        float* st = L.stat + tid * 5;
-        st[0] = policyLoss;
-        st[1] = 0.5f * a.hp.value_coef * vErr * vErr;
-        st[2] = entropy;
-        st[3] = oldLp - logpA;
-        st[4] = (fabsf(ratio - 1.0f) > clip) ? 1.0f : 0.0f;
-        if (a.head_out)
-            for (int j = 0; j < HD; ++j) a.head_out[(size_t)(r0 + tid) * HD + j] = h[j];
+        if (lk == 0) {
+            const float vErr = h[A] - ret;
+            dz[A] = a.hp.value_coef * vErr * scale;
+            float* st = L.stat + lrow * 5;
+            st[0] = -(surr1 < surr2 ? surr1 : surr2);
+            st[1] = 0.5f * a.hp.value_coef * vErr * vErr;
+            st[2] = entropy;
+            st[3] = oldLp - logpA;
+            st[4] = (fabsf(ratio - 1.0f) > clip) ? 1.0f : 0.0f;
+        }
+        if (a.head_out) {
+            if (j0 < HD) a.head_out[(size_t)(r0 + lrow) * HD + j0] = h[j0];
+            if (j1 < HD) a.head_out[(size_t)(r0 + lrow) * HD + j1] = h[j1];
+        }
     }
     __syncthreads();
 
