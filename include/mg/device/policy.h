@@ -301,11 +301,11 @@ __device__ __forceinline__ void store_tile_g(const AccTile<M, W>& acc, float* gl
 }
 
 // model/input.metal:11-27: h = b_in + sum_k obs[k] W_in[k], in k order.
-// obsL is [M][O] in LDS.
+// obsL is [M][O] in LDS; Win ([O][128]) and bias ([128]) are in global memory
+// or LDS.
 template <int M, int W = 4>
-__device__ __forceinline__ void fwd_embed(const mg_policy_view& pv, const float* obsL, int O, FwdRegs<M, W>& R) {
-    const float* Win = pv.params + pv.off_in_w;
-    const float* bias = pv.params + pv.off_in_b;
+__device__ __forceinline__ void fwd_embed(const float* Win, const float* bias, const float* obsL, int O,
+                                          FwdRegs<M, W>& R) {
     for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) { R.h[rt][ct][r] = bias[col]; });
     for (int k = 0; k < O; ++k) {
         for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
@@ -445,7 +445,7 @@ __device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem
     const Seq seq{&pv, NC};
     Stream ws;
     ws.start(2 * (int)pv.layers * NC, seq);
-    fwd_embed<M, W>(pv, obsL, O, R);
+    fwd_embed<M, W>(pv.params + pv.off_in_w, pv.params + pv.off_in_b, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
         fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l]);
         fwd_block<M, W, false, 1, Seq>(pv, (int)l, sm, R, ws, nullptr, seq);

@@ -240,6 +240,13 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     // weight stream issued after it (vector memory counters complete in order).
     for (int idx = tid; idx < M * O; idx += kTNT) L.obs[idx] = a.obs_slots[g0 * O + idx];
     for (int idx = tid; idx < kEmbed * HD; idx += kTNT) L.wh[idx] = pv.params[pv.off_head + idx];
+    // W_in and b_in for the embed, in the LN capture area (first written by the
+    // first LN, after every wave is done with the embed)
+    float* winL = L.xn;
+    float* binL = L.xn + kMaxObsT * kEmbed;
+    static_assert((kMaxObsT + 1) * kEmbed <= (MG_MAX_LAYERS + 1) * kTR * kEmbed, "embed staging fits");
+    for (int idx = tid; idx < O * kEmbed; idx += kTNT) winL[idx] = pv.params[pv.off_in_w + idx];
+    if (tid < kEmbed) binL[tid] = pv.params[pv.off_in_b + tid];
     for (int idx = tid; idx < (NL + 1) * 2 * kEmbed; idx += kTNT) {
         const int ln = idx / (2 * kEmbed), k = idx % (2 * kEmbed);
         L.ln[idx] = k < kEmbed ? pv.params[pv.off_ln_gamma[ln] + k] : pv.params[pv.off_ln_beta[ln] + k - kEmbed];
@@ -262,7 +269,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     __syncthreads();
 
     // ---- forward with capture ----
-    fwd_embed<M, kTW>(pv, L.obs, O, R);
+    fwd_embed<M, kTW>(winL, binL, L.obs, O, R);
     for (int l = 0; l < NL; ++l) {
         fwd_layernorm<M, kTW>(sm, R, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, L.xn + l * M * kEmbed,
                               L.sd + l * M, ws.x + ((size_t)l * B + r0) * kEmbed);
