@@ -411,7 +411,7 @@ struct DwArgs {
     uint32_t tiles_per_big[kMaxBig];
     uint32_t big_tiles;    // total 64x64 tiles over all big matrices
     uint32_t rows;         // B
-    uint32_t splits;       // row splits (gridDim.y)
+    uint32_t splits;       // row splits
     uint32_t count;        // arena length
     float* partial;
 };
@@ -419,16 +419,20 @@ struct DwArgs {
 constexpr int kDwRows = 32;    // rows staged in LDS per step
 constexpr int kDwLd = 64 + 4;  // LDS row stride of a staged 64-wide slab
 
+// Workgroup id = tile * splits + split: workgroups go to the 8 XCDs round
+// robin, so with 8 or 16 splits all tiles of one row split run on the same XCD
+// and read its rows through that XCD's L2 (each row is fetched from memory
+// about once instead of once per tile sharing it).
 __global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
     __shared__ float xs[2][kDwRows * kDwLd];
     __shared__ float ys[2][kDwRows * kDwLd];
-    const uint32_t split = blockIdx.y;
+    const uint32_t split = blockIdx.x % a.splits, tile = blockIdx.x / a.splits;
     const uint32_t rowsPer = a.rows / a.splits;
     const uint32_t rb = split * rowsPer;
     float* out = a.partial + (size_t)split * a.count;
     const int tid = threadIdx.x;
-    if (blockIdx.x < a.big_tiles) {
-        uint32_t t = blockIdx.x, m = 0;
+    if (tile < a.big_tiles) {
+        uint32_t t = tile, m = 0;
         while (t >= a.tiles_per_big[m]) t -= a.tiles_per_big[m], ++m;
         const BigMat& bm = a.big[m];
         const uint32_t ntn = bm.ndim / 64;
@@ -849,7 +853,7 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         }
         da.nbig = nb;
         da.big_tiles = tiles;
-        hipLaunchKernelGGL(dev::train_dw_kernel, dim3(tiles, splits), dim3(256), 0, st, da);
+        hipLaunchKernelGGL(dev::train_dw_kernel, dim3(tiles * splits), dim3(256), 0, st, da);
         MG_HIP(hipGetLastError(), "train dW launch");
     }
     {  // 3. gradient assembly + partial norms
