@@ -66,10 +66,12 @@ def bench_collect(kernel, n, T, steps, warmup, O, A):
     return gym, model, dt, times
 
 
-def bench_random(n, T, reps):
+def bench_random(n, T, reps, kernel="rollout_cartpole", hbm=True):
+    """Random-policy rollouts; the HBM figures are CartPole's slot and state
+    bytes (26.5 B per env-step)."""
     import metalgym_amd as mg
 
-    gym = mg.Gym("rollout_cartpole", n, 0)
+    gym = mg.Gym(kernel, n, 0)
     bufs = gym.rollout_random(T)
     sync()
     mg.timing_reset()
@@ -82,9 +84,12 @@ def bench_random(n, T, reps):
     mg.timing_enable(False)
     times = mg.timing_get()
     kms = kernel_avg_ms(times, "rollout")
-    bytes_launch = n * T * 25 + n * 2 * (20 + 4 + 1)
-    return {"env_steps_per_s": reps * n * T / dt, "kernel_us": kms * 1e3,
-            "hbm_GBps": bytes_launch / (kms * 1e-3) / 1e9, "hbm_frac": bytes_launch / (kms * 1e-3) / PEAK_HBM}
+    out = {"env_steps_per_s": reps * n * T / dt, "kernel_us": kms * 1e3}
+    if hbm:
+        bytes_launch = n * T * 25 + n * 2 * (20 + 4 + 1)
+        out["hbm_GBps"] = bytes_launch / (kms * 1e-3) / 1e9
+        out["hbm_frac"] = bytes_launch / (kms * 1e-3) / PEAK_HBM
+    return out
 
 
 def bench_full(kernel, n, T, iters, O, A, epochs=4):
@@ -270,6 +275,20 @@ def main():
         extra["voxelnav16_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtv,
                                               "collect_ms": kernel_avg_ms(tv, "collect")}
         extra["voxelnav16_full_ppo_262144"] = bench_full("rollout_voxelnav16", 262144, 32, 1, 30, 6)
+        # the reference's heightmap VoxelNav at its README configuration (4096 envs,
+        # 2-block policy; published Apple M4 figures: 7.9 M, 2.4 M, 265 K)
+        vr = bench_random(4096, 32, 20, "rollout_voxelnav", hbm=False)
+        vr["vs_published_m4_7.9M"] = vr["env_steps_per_s"] / 7.9e6
+        extra["voxelnav_random_4096"] = vr
+        _, _, dtr, _ = bench_collect("rollout_voxelnav", 4096, 32, 10, 2, 40, 6)
+        extra["voxelnav_collect_4096"] = {"env_steps_per_s": 10 * 4096 * 32 / dtr,
+                                          "vs_published_m4_2.4M": 10 * 4096 * 32 / dtr / 2.4e6}
+        extra["voxelnav_full_ppo_4096"] = bench_full("rollout_voxelnav", 4096, 32, 3, 40, 6)
+        extra["voxelnav_full_ppo_4096"]["vs_published_m4_265K"] = \
+            extra["voxelnav_full_ppo_4096"]["env_steps_per_s"] / 265e3
+        extra["voxelnav_random_262144"] = bench_random(262144, 32, 5, "rollout_voxelnav", hbm=False)
+        _, _, dtr2, _ = bench_collect("rollout_voxelnav", 262144, 32, 3, 1, 40, 6)
+        extra["voxelnav_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtr2}
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

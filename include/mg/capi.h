@@ -63,7 +63,8 @@ int mg_synchronize(void);
  * kernels are instantiated by MG_DEFINE_ENV (mg/device/env_kernels.h), which
  * registers this table under Env::KERNEL. The built-in envs are
  * "rollout_cartpole", "rollout_cartpole_continuous",
- * "rollout_cartpole_continuous_clamp" and "rollout_voxelnav16".
+ * "rollout_cartpole_continuous_clamp", "rollout_voxelnav" (the reference's
+ * heightmap env) and "rollout_voxelnav16".
  * ------------------------------------------------------------------------- */
 
 enum { MG_ACTIONS_GIVEN = 0, MG_ACTIONS_RANDOM = 1 };

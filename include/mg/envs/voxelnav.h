@@ -1,0 +1,203 @@
+// VoxelNav: the reference's heightmap navigation env
+// (examples/VoxelNav/voxelnav.metal:9-174), after minetrix's bridge task. A
+// 32 x 32 heightmap (uint8 heights, 0 = void) of rolling hills with one chasm
+// along z; the agent spawns on the near side, the goal is on the far side; it
+// walks, turns, jumps or places cobble to cross. The observation is a depth
+// camera of 8 x 4 rays marched through the heightmap plus the goal in the
+// agent's frame. Same State / Obs layout, constants, RNG draw order and
+// arithmetic order as the reference; its Metal sin / cos are replaced by the
+// deterministic mg::sinf / mg::cosf so the host oracle and the GPU agree bit
+// for bit (the reference's own fast-math bits are not reproducible here).
+//
+// The state is 1 KB per env (the heightmap), so the rollout kernels update it
+// in place in device memory.
+#pragma once
+#include <math.h>
+
+#include "../env.h"
+#include "../math.h"
+
+struct VoxelNav {
+    static constexpr uint32_t W = 32;
+    static constexpr uint32_t RAY_COLS = 8;
+    static constexpr uint32_t RAY_ROWS = 4;
+    static constexpr uint32_t N_RAYS = RAY_COLS * RAY_ROWS;
+    static constexpr uint32_t OBS_DIM = N_RAYS + 8;
+    static constexpr uint32_t ACT_DIM = 6;
+    static constexpr uint32_t MAX_STEPS = 250;
+    static constexpr float PI = 3.14159265358979323846f;  // Metal's M_PI_F
+    static constexpr float FOV = 90.0f * PI / 180.0f;
+    static constexpr float MAX_DEPTH = 24.0f;
+    static constexpr float EYE = 1.6f;
+    static constexpr float GOAL_RADIUS = 1.5f;
+    static constexpr uint32_t START_COBBLE = 16;
+    static constexpr const char* KERNEL = "rollout_voxelnav";
+
+    struct State {
+        float x, z, yaw;
+        float gx, gz;
+        float prevDist;
+        uint32_t steps;
+        uint32_t cobble;
+        uint8_t height[W * W];  // terrain height per cell (x-major), 0 = void
+    };
+    using Action = int;  // 0 forward, 1 back, 2 turn left, 3 turn right, 4 jump forward, 5 place cobble
+    struct Obs {
+        float ray[N_RAYS];  // depth / MAX_DEPTH, ray c * RAY_ROWS + r
+        float goalForward, goalRight, goalUp, goalDist;
+        float sinYaw, cosYaw, cobble, height;
+    };
+
+    MG_HD static uint32_t cell(int cx, int cz) { return (uint32_t)cx * W + (uint32_t)cz; }
+    MG_HD static bool inside(int cx, int cz) { return cx >= 0 && cz >= 0 && cx < (int)W && cz < (int)W; }
+    MG_HD static float heightAt(const State& s, float x, float z) {
+        const int cx = (int)floorf(x), cz = (int)floorf(z);
+        return inside(cx, cz) ? (float)s.height[cell(cx, cz)] : 0.0f;
+    }
+    MG_HD static float dist(const State& s) {
+        const float dx = s.gx - s.x, dz = s.gz - s.z;
+        return sqrtf(dx * dx + dz * dz);
+    }
+    // Metal's mix(x, y, a) = x + (y - x) a
+    MG_HD static float mix(float x, float y, float a) { return x + (y - x) * a; }
+
+    MG_HD static void reset(State& s, uint32_t& rng) {
+        // rolling hills: 5 x 5 random knots, bilinear between them
+        float knot[25];
+        for (uint32_t i = 0; i < 25; i++) knot[i] = rngUniform(rng, 3.0f, 9.0f);
+        for (uint32_t cx = 0; cx < W; cx++) {
+            const float fx = (float)cx / (float)(W - 1) * 4.0f;
+            const uint32_t ix = (uint32_t)fx < 3u ? (uint32_t)fx : 3u;
+            const float tx = fx - (float)ix;
+            for (uint32_t cz = 0; cz < W; cz++) {
+                const float fz = (float)cz / (float)(W - 1) * 4.0f;
+                const uint32_t iz = (uint32_t)fz < 3u ? (uint32_t)fz : 3u;
+                const float tz = fz - (float)iz;
+                const float h = mix(mix(knot[ix * 5 + iz], knot[(ix + 1) * 5 + iz], tx),
+                                    mix(knot[ix * 5 + iz + 1], knot[(ix + 1) * 5 + iz + 1], tx), tz);
+                s.height[cell((int)cx, (int)cz)] = (uint8_t)roundf(h);
+            }
+        }
+        // one chasm along z, 2 to 5 cells wide; the far side may be lifted
+        const uint32_t width = 2 + rngInt(rng, 4);
+        const uint32_t left = 12 + rngInt(rng, 6);
+        const uint32_t lift = rngInt(rng, 3);
+        for (uint32_t cx = 0; cx < W; cx++) {
+            for (uint32_t cz = 0; cz < W; cz++) {
+                const uint32_t k = cell((int)cx, (int)cz);
+                if (cx >= left && cx < left + width) {
+                    s.height[k] = 0;
+                } else if (cx >= left + width) {
+                    const uint32_t lifted = (uint32_t)s.height[k] + lift;
+                    s.height[k] = (uint8_t)(lifted < 15u ? lifted : 15u);
+                }
+            }
+        }
+        s.x = 2.5f + rngUniform(rng) * (float)(left - 4);
+        s.z = 2.5f + rngUniform(rng) * (float)(W - 5);
+        s.gx = (float)(left + width) + 2.5f + rngUniform(rng) * (float)(W - 5 - (left + width));
+        s.gz = 2.5f + rngUniform(rng) * (float)(W - 5);
+        s.yaw = rngUniform(rng, -PI, PI);
+        s.prevDist = dist(s);
+        s.steps = 0;
+        s.cobble = START_COBBLE;
+    }
+
+    MG_HD static void observe(const State& s, Obs& o) {
+        const float pitches[RAY_ROWS] = {-45.0f, -20.0f, 0.0f, 15.0f};
+        const float h = heightAt(s, s.x, s.z);
+        const float ey = h + EYE;
+        for (uint32_t c = 0; c < RAY_COLS; c++) {
+            const float a = s.yaw + ((float)c / (float)(RAY_COLS - 1) - 0.5f) * FOV;
+            const float ca = mg::cosf(a), sa = mg::sinf(a);
+            for (uint32_t r = 0; r < RAY_ROWS; r++) {
+                const float p = pitches[r] * PI / 180.0f;
+                const float cp = mg::cosf(p);
+                const float dx = cp * ca, dy = mg::sinf(p), dz = cp * sa;
+                float depth = MAX_DEPTH;
+                for (float t = 0.5f; t < MAX_DEPTH; t += 0.5f) {
+                    const float px = s.x + t * dx, py = ey + t * dy, pz = s.z + t * dz;
+                    const int cx = (int)floorf(px), cz = (int)floorf(pz);
+                    if (!inside(cx, cz)) {
+                        depth = t;
+                        break;
+                    }
+                    if (py <= (float)s.height[cell(cx, cz)]) {
+                        depth = t;
+                        break;
+                    }
+                }
+                o.ray[c * RAY_ROWS + r] = depth / MAX_DEPTH;
+            }
+        }
+        const float gx = s.gx - s.x, gz = s.gz - s.z;
+        const float ca = mg::cosf(s.yaw), sa = mg::sinf(s.yaw);
+        o.goalForward = (gx * ca + gz * sa) / (float)W;
+        o.goalRight = (-gx * sa + gz * ca) / (float)W;
+        o.goalUp = (heightAt(s, s.gx, s.gz) - h) / 8.0f;
+        o.goalDist = sqrtf(gx * gx + gz * gz) / (float)W;
+        o.sinYaw = sa;
+        o.cosYaw = ca;
+        o.cobble = (float)s.cobble / (float)START_COBBLE;
+        o.height = h / 16.0f;
+    }
+
+    // Moves to (nx, nz) if the target cell is solid and at most one block up;
+    // returns true if the move ended in the void.
+    MG_HD static bool tryMove(State& s, float nx, float nz) {
+        const int cx = (int)floorf(nx), cz = (int)floorf(nz);
+        if (!inside(cx, cz)) return false;
+        const float here = heightAt(s, s.x, s.z);
+        const float there = (float)s.height[cell(cx, cz)];
+        if (there == 0.0f) {
+            s.x = nx;
+            s.z = nz;
+            return true;
+        }
+        if (there > here + 1.0f) return false;
+        s.x = nx;
+        s.z = nz;
+        return false;
+    }
+
+    MG_HD static void step(State& s, Action action, Obs& obs, float& reward, uint8_t& done) {
+        const float ca = mg::cosf(s.yaw), sa = mg::sinf(s.yaw);
+        bool fell = false;
+        switch (action) {
+            case 0: fell = tryMove(s, s.x + ca, s.z + sa); break;
+            case 1: fell = tryMove(s, s.x - ca, s.z - sa); break;
+            case 2: s.yaw -= PI / 6.0f; break;
+            case 3: s.yaw += PI / 6.0f; break;
+            case 4: fell = tryMove(s, s.x + 2.0f * ca, s.z + 2.0f * sa); break;
+            case 5: {
+                const int cx = (int)floorf(s.x + ca), cz = (int)floorf(s.z + sa);
+                if (s.cobble > 0 && inside(cx, cz)) {
+                    const uint32_t k = cell(cx, cz);
+                    const uint32_t here = (uint32_t)heightAt(s, s.x, s.z);
+                    if (s.height[k] == 0) {
+                        s.height[k] = (uint8_t)here;
+                        s.cobble--;
+                    } else if ((uint32_t)s.height[k] <= here) {
+                        s.height[k]++;
+                        s.cobble--;
+                    }
+                }
+                break;
+            }
+            default: break;
+        }
+        if (s.yaw > PI) s.yaw -= 2.0f * PI;
+        if (s.yaw < -PI) s.yaw += 2.0f * PI;
+        s.steps++;
+
+        const float d = dist(s);
+        const float prog = s.prevDist - d;
+        reward = -0.05f + 0.2f * (prog < -1.5f ? -1.5f : (prog > 1.5f ? 1.5f : prog));
+        s.prevDist = d;
+        const bool success = d < GOAL_RADIUS;
+        if (success) reward += 10.0f;
+        if (fell) reward -= 5.0f;
+        done = (success || fell || s.steps >= MAX_STEPS) ? 1 : 0;
+        observe(s, obs);
+    }
+};

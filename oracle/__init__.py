@@ -15,12 +15,13 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "build", "liboracle.so")
 
-CARTPOLE, CARTPOLE_CONT, CARTPOLE_CONT_CLAMP, VOXELNAV16 = 0, 1, 2, 3
+CARTPOLE, CARTPOLE_CONT, CARTPOLE_CONT_CLAMP, VOXELNAV16, VOXELNAV = 0, 1, 2, 3, 4
 ENV_KERNELS = {
     CARTPOLE: "rollout_cartpole",
     CARTPOLE_CONT: "rollout_cartpole_continuous",
     CARTPOLE_CONT_CLAMP: "rollout_cartpole_continuous_clamp",
     VOXELNAV16: "rollout_voxelnav16",
+    VOXELNAV: "rollout_voxelnav",
 }
 
 

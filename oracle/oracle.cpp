@@ -153,6 +153,159 @@ void vn_step(VNState& s, int action, float* obs, float& reward, uint8_t& done) {
     obs[29] = (float)(s.gz - s.pz) / 15.0f;
 }
 
+// ---- VoxelNav: examples/VoxelNav/voxelnav.metal:9-174 ----------------------
+// Heightmap 32 x 32 (index cx * 32 + cz), 8 x 4 depth rays, 6 actions. The
+// reference's Metal cos / sin are replaced by mg::cosf / mg::sinf (the
+// product's deterministic functions).
+const int kVW = 32;
+const float kVPi = 3.14159265358979323846f;
+const float kVFov = 90.0f * kVPi / 180.0f;
+const float kVMaxDepth = 24.0f;
+struct VRState {
+    float x, z, yaw, gx, gz, prevDist;
+    uint32_t steps, cobble;
+    uint8_t height[kVW * kVW];
+};
+
+bool vr_inside(int cx, int cz) { return cx >= 0 && cz >= 0 && cx < kVW && cz < kVW; }
+
+float vr_height(const VRState& s, float x, float z) {  // voxelnav.metal:40-43
+    int cx = (int)std::floor(x), cz = (int)std::floor(z);
+    return vr_inside(cx, cz) ? (float)s.height[cx * kVW + cz] : 0.0f;
+}
+
+float vr_dist(const VRState& s) {  // voxelnav.metal:44-47
+    float dx = s.gx - s.x, dz = s.gz - s.z;
+    return std::sqrt(dx * dx + dz * dz);
+}
+
+float vr_lerp(float a, float b, float t) { return a + (b - a) * t; }  // Metal mix()
+
+void vr_reset(VRState& s, uint32_t& rng) {  // voxelnav.metal:49-83
+    float knot[25];
+    for (int i = 0; i < 25; ++i) knot[i] = xs_unif(rng, 3.0f, 9.0f);
+    for (int cx = 0; cx < kVW; ++cx) {
+        float fx = (float)cx / (float)(kVW - 1) * 4.0f;
+        int ix = std::min((int)fx, 3);
+        float tx = fx - (float)ix;
+        for (int cz = 0; cz < kVW; ++cz) {
+            float fz = (float)cz / (float)(kVW - 1) * 4.0f;
+            int iz = std::min((int)fz, 3);
+            float tz = fz - (float)iz;
+            float lo = vr_lerp(knot[ix * 5 + iz], knot[(ix + 1) * 5 + iz], tx);
+            float hi = vr_lerp(knot[ix * 5 + iz + 1], knot[(ix + 1) * 5 + iz + 1], tx);
+            s.height[cx * kVW + cz] = (uint8_t)std::round(vr_lerp(lo, hi, tz));
+        }
+    }
+    uint32_t width = 2 + xs_next(rng) % 4u;
+    uint32_t left = 12 + xs_next(rng) % 6u;
+    uint32_t lift = xs_next(rng) % 3u;
+    for (uint32_t cx = 0; cx < (uint32_t)kVW; ++cx)
+        for (int cz = 0; cz < kVW; ++cz) {
+            uint8_t& h = s.height[cx * kVW + cz];
+            if (cx >= left && cx < left + width)
+                h = 0;
+            else if (cx >= left + width)
+                h = (uint8_t)std::min<uint32_t>(h + lift, 15u);
+        }
+    s.x = 2.5f + xs_unif(rng) * (float)(left - 4);
+    s.z = 2.5f + xs_unif(rng) * (float)(kVW - 5);
+    s.gx = (float)(left + width) + 2.5f + xs_unif(rng) * (float)(kVW - 5 - (int)(left + width));
+    s.gz = 2.5f + xs_unif(rng) * (float)(kVW - 5);
+    s.yaw = xs_unif(rng, -kVPi, kVPi);
+    s.prevDist = vr_dist(s);
+    s.steps = 0;
+    s.cobble = 16;
+}
+
+void vr_observe(const VRState& s, float* obs) {  // voxelnav.metal:85-115
+    static const float pitchDeg[4] = {-45.0f, -20.0f, 0.0f, 15.0f};
+    float h = vr_height(s, s.x, s.z);
+    float eye = h + 1.6f;
+    for (int c = 0; c < 8; ++c) {
+        float a = s.yaw + ((float)c / 7.0f - 0.5f) * kVFov;
+        float cosA = mg::cosf(a), sinA = mg::sinf(a);
+        for (int r = 0; r < 4; ++r) {
+            float p = pitchDeg[r] * kVPi / 180.0f;
+            float cosP = mg::cosf(p);
+            float dx = cosP * cosA, dy = mg::sinf(p), dz = cosP * sinA;
+            float depth = kVMaxDepth;
+            for (float t = 0.5f; t < kVMaxDepth; t += 0.5f) {
+                float px = s.x + t * dx, py = eye + t * dy, pz = s.z + t * dz;
+                int cx = (int)std::floor(px), cz = (int)std::floor(pz);
+                if (!vr_inside(cx, cz) || py <= (float)s.height[cx * kVW + cz]) {
+                    depth = t;
+                    break;
+                }
+            }
+            obs[c * 4 + r] = depth / kVMaxDepth;
+        }
+    }
+    float gx = s.gx - s.x, gz = s.gz - s.z;
+    float cy = mg::cosf(s.yaw), sy = mg::sinf(s.yaw);
+    obs[32] = (gx * cy + gz * sy) / (float)kVW;
+    obs[33] = (-gx * sy + gz * cy) / (float)kVW;
+    obs[34] = (vr_height(s, s.gx, s.gz) - h) / 8.0f;
+    obs[35] = std::sqrt(gx * gx + gz * gz) / (float)kVW;
+    obs[36] = sy;
+    obs[37] = cy;
+    obs[38] = (float)s.cobble / 16.0f;
+    obs[39] = h / 16.0f;
+}
+
+// voxelnav.metal:119-129; true when the move ends in the void
+bool vr_move(VRState& s, float nx, float nz) {
+    int cx = (int)std::floor(nx), cz = (int)std::floor(nz);
+    if (!vr_inside(cx, cz)) return false;
+    float here = vr_height(s, s.x, s.z);
+    float there = (float)s.height[cx * kVW + cz];
+    if (there != 0.0f && there > here + 1.0f) return false;
+    s.x = nx;
+    s.z = nz;
+    return there == 0.0f;
+}
+
+void vr_step(VRState& s, int action, float* obs, float& reward, uint8_t& done) {  // voxelnav.metal:131-162
+    float cy = mg::cosf(s.yaw), sy = mg::sinf(s.yaw);
+    bool fell = false;
+    if (action == 0) {
+        fell = vr_move(s, s.x + cy, s.z + sy);
+    } else if (action == 1) {
+        fell = vr_move(s, s.x - cy, s.z - sy);
+    } else if (action == 2) {
+        s.yaw -= kVPi / 6.0f;
+    } else if (action == 3) {
+        s.yaw += kVPi / 6.0f;
+    } else if (action == 4) {
+        fell = vr_move(s, s.x + 2.0f * cy, s.z + 2.0f * sy);
+    } else if (action == 5) {
+        int cx = (int)std::floor(s.x + cy), cz = (int)std::floor(s.z + sy);
+        if (s.cobble > 0 && vr_inside(cx, cz)) {
+            uint8_t& t = s.height[cx * kVW + cz];
+            uint32_t here = (uint32_t)vr_height(s, s.x, s.z);
+            if (t == 0) {
+                t = (uint8_t)here;
+                s.cobble -= 1;
+            } else if ((uint32_t)t <= here) {
+                t = (uint8_t)(t + 1);
+                s.cobble -= 1;
+            }
+        }
+    }
+    if (s.yaw > kVPi) s.yaw -= 2.0f * kVPi;
+    if (s.yaw < -kVPi) s.yaw += 2.0f * kVPi;
+    s.steps += 1;
+    float d = vr_dist(s);
+    float progress = std::min(1.5f, std::max(-1.5f, s.prevDist - d));
+    reward = -0.05f + 0.2f * progress;
+    s.prevDist = d;
+    bool success = d < 1.5f;
+    if (success) reward += 10.0f;
+    if (fell) reward -= 5.0f;
+    done = (success || fell || s.steps >= 250) ? 1 : 0;
+    vr_observe(s, obs);
+}
+
 // ---- env dispatch -----------------------------------------------------------
 orc_env_info env_info(int env) {
     switch (env) {
@@ -160,6 +313,7 @@ orc_env_info env_info(int env) {
         case ORC_CARTPOLE_CONT:
         case ORC_CARTPOLE_CONT_CLAMP: return {sizeof(CPState), 4, 4, 1, 1};
         case ORC_VOXELNAV16: return {sizeof(VNState), 4, 30, 6, 0};
+        case ORC_VOXELNAV: return {sizeof(VRState), 4, 40, 6, 0};
         default: return {0, 0, 0, 0, 0};
     }
 }
@@ -167,6 +321,8 @@ orc_env_info env_info(int env) {
 void env_reset(int env, void* state, uint32_t& rng) {
     if (env == ORC_VOXELNAV16)
         vn_reset(*static_cast<VNState*>(state), rng);
+    else if (env == ORC_VOXELNAV)
+        vr_reset(*static_cast<VRState*>(state), rng);
     else
         cp_reset(*static_cast<CPState*>(state), rng);
 }
@@ -196,6 +352,12 @@ void env_step(int env, void* state, const void* action, float* obs, float& rewar
             int a;
             std::memcpy(&a, action, 4);
             vn_step(*static_cast<VNState*>(state), a, obs, reward, done);
+            break;
+        }
+        case ORC_VOXELNAV: {
+            int a;
+            std::memcpy(&a, action, 4);
+            vr_step(*static_cast<VRState*>(state), a, obs, reward, done);
             break;
         }
     }

@@ -19,7 +19,7 @@ extern "C" {
 #endif
 
 /* env ids */
-enum { ORC_CARTPOLE = 0, ORC_CARTPOLE_CONT = 1, ORC_CARTPOLE_CONT_CLAMP = 2, ORC_VOXELNAV16 = 3 };
+enum { ORC_CARTPOLE = 0, ORC_CARTPOLE_CONT = 1, ORC_CARTPOLE_CONT_CLAMP = 2, ORC_VOXELNAV16 = 3, ORC_VOXELNAV = 4 };
 
 typedef struct orc_env_info {
     uint32_t state_bytes;

@@ -10,6 +10,7 @@ ENVS = {
     "cartpole_continuous": (1, "rollout_cartpole_continuous"),
     "cartpole_continuous_clamp": (2, "rollout_cartpole_continuous_clamp"),
     "voxelnav16": (3, "rollout_voxelnav16"),
+    "voxelnav": (4, "rollout_voxelnav"),
 }
 
 TOL_HEAD = 1e-4     # policy head, values, GAE

@@ -33,3 +33,13 @@ def test_reference_training_loop_runs():
     assert p.returncode == 0
     lines = [l for l in p.stdout.splitlines() if l.startswith("iter")]
     assert len(lines) == 4
+
+
+def test_voxelnav_learns():
+    """The reference's VoxelNav loop (examples/VoxelNav/main.cpp): the success
+    rate (episodes ending with reward > 5) rises well above its start."""
+    p = run("voxelnav", "150", timeout=300)
+    assert p.returncode == 0
+    rates = [float(l.split()[3]) for l in p.stdout.splitlines() if l.startswith("iter")]
+    assert len(rates) >= 10
+    assert max(rates[-3:]) > max(0.3, 3 * rates[0]), rates

@@ -20,6 +20,7 @@ def compare_gym(gym, g, what):
     ("cartpole_continuous", 2048, 64, 0),
     ("cartpole_continuous_clamp", 2048, 64, 1),
     ("voxelnav16", 512, 300, 0),          # past the 256-step cap
+    ("voxelnav", 512, 300, 2),            # past the 250-step cap
 ])
 def test_random_rollout_bit_exact(mg, orc, env, n, steps, seed):
     eid, kernel = ENVS[env]
@@ -38,7 +39,7 @@ def test_random_rollout_bit_exact(mg, orc, env, n, steps, seed):
     assert dn.any(), "no episode ended: the test does not exercise resets"
 
 
-@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "voxelnav16"])
+@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "voxelnav16", "voxelnav"])
 def test_given_action_rollout_bit_exact(mg, orc, env):
     eid, kernel = ENVS[env]
     n, steps = 2048, 40

@@ -125,6 +125,7 @@ def float64_moment(pv, params, rows, hp):
     ("cartpole", 1280, 2, 320, 3, 2, 4),      # minibatch not a multiple of 128
     ("cartpole_continuous", 2048, 2, 1024, 2, 2, 4),
     ("voxelnav16", 1024, 2, 512, 1, 2, 4),
+    ("voxelnav", 1024, 2, 512, 1, 2, 4),
     ("cartpole", 1024, 2, 512, 2, 3, 2),      # hidden 256, three blocks
     ("cartpole", 1024, 2, 512, 1, 5, 2),      # five blocks
     ("cartpole", 1024, 2, 512, 0, 8, 1),      # the most blocks (MG_MAX_LAYERS), hidden 128
