@@ -63,7 +63,10 @@ int launch_rollout(const mg_rollout_args* a) {
     if (!a || a->n == 0 || !a->state || !a->rng || !a->done) return MG_ERR_INVALID;
     if (a->steps == 0) return 0;
     if (a->mode == MG_ACTIONS_GIVEN && !a->actions_in) return MG_ERR_INVALID;
-    dim3 block(256), grid((a->n + 255) / 256);
+    // one lane per env: below 64 K envs one-wave workgroups spread the waves
+    // over more CUs (4096 envs are 64 waves: 64 CUs instead of 16)
+    const uint32_t bs = a->n >= 65536u ? 256u : 64u;
+    dim3 block(bs), grid((a->n + bs - 1) / bs);
     hipStream_t st = static_cast<hipStream_t>(a->stream);
     if (a->mode == MG_ACTIONS_RANDOM)
         hipLaunchKernelGGL((rollout_kernel<Env, MG_ACTIONS_RANDOM>), grid, block, 0, st, *a);
