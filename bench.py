@@ -46,11 +46,11 @@ def kernel_avg_ms(times, k):
     return tot / cnt if cnt else float("nan")
 
 
-def bench_collect(kernel, n, T, steps, warmup, O, A):
+def bench_collect(kernel, n, T, steps, warmup, O, A, precision="fp32"):
     import metalgym_amd as mg
 
     gym = mg.Gym(kernel, n, 0)
-    model = mg.PPOModel(gym, horizon=T)
+    model = mg.PPOModel(gym, horizon=T, precision=precision)
     for _ in range(warmup):
         model.collect()
     sync()
@@ -289,6 +289,14 @@ def main():
         extra["voxelnav_random_262144"] = bench_random(262144, 32, 5, "rollout_voxelnav", hbm=False)
         _, _, dtr2, _ = bench_collect("rollout_voxelnav", 262144, 32, 3, 1, 40, 6)
         extra["voxelnav_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtr2}
+        # bf16 matrix operands (the reference's matmul precision), policy forward only
+        _, _, dtb, tb = bench_collect("rollout_cartpole", 262144, 32, 5, 2, O, A, precision="bf16")
+        kb = kernel_avg_ms(tb, "collect")
+        extra["bf16_collect_262144"] = {"env_steps_per_s": 5 * 262144 * 32 / dtb, "collect_ms": kb,
+                                        "matmul_TFLOPs": flop_launch / (kb * 1e-3) / 1e12}
+        _, _, dtb4, _ = bench_collect("rollout_cartpole", 4096, 32, 20, 2, O, A, precision="bf16")
+        extra["bf16_collect_4096"] = {"env_steps_per_s": 20 * 4096 * 32 / dtb4,
+                                      "vs_published_m4_3.8M": 20 * 4096 * 32 / dtb4 / 3.8e6}
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

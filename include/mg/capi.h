@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MG_ABI_VERSION 3
+#define MG_ABI_VERSION 4
 #define MG_MAX_LAYERS 8
 #define MG_EMBED 128 /* the reference's N_EMBED_CFG (model/config.h:7) */
 
@@ -105,14 +105,21 @@ typedef struct mg_rollout_args {
  * (k % 128 / KG) 256 + (k % KG / 4) 4 MT + (n % MT) 4 + k % 4 from the
  * matrix's offset (MT = 32, KG = 8 for 32x32x2; MT = 16, KG = 16 for 16x16x4).
  * frag_fwd32 and frag_fwd16 hold up^T and down^T (the forward's operands),
- * frag_bwd16 up and down as stored (the backward's). The library derives them
+ * frag_bwd16 up and down as stored (the backward's). With precision
+ * MG_PRECISION_BF16, frag_fwd32_bf and frag_fwd16_bf hold up^T and down^T
+ * rounded to bfloat16 (16-bit patterns) in the operand order of the bf16
+ * instructions (32x32x16 and 16x16x32: k-groups of 16 and 32, each lane 8
+ * consecutive k); otherwise they are NULL. The library derives all of them
  * from params at creation, in every Adam step and in mg_ppo_set_params /
  * mg_ppo_params_updated; the fused kernels read the matrices from them. */
+enum { MG_PRECISION_FP32 = 0, MG_PRECISION_BF16 = 1 };
 typedef struct mg_policy_view {
     float* params;
     float* frag_fwd32;
     float* frag_fwd16;
     float* frag_bwd16;
+    uint16_t* frag_fwd32_bf;
+    uint16_t* frag_fwd16_bf;
     uint32_t obs_dim;
     uint32_t act_dim;
     uint32_t embed;
@@ -120,7 +127,8 @@ typedef struct mg_policy_view {
     uint32_t layers;
     uint32_t head_dim;
     uint32_t continuous;
-    uint32_t count; /* arena length in floats */
+    uint32_t precision; /* MG_PRECISION_*: the policy forward's matrix operands */
+    uint32_t count;     /* arena length in floats */
     uint32_t off_in_w;
     uint32_t off_in_b;
     uint32_t off_ln_gamma[MG_MAX_LAYERS + 1]; /* index `layers` = final LN */
@@ -232,7 +240,12 @@ typedef struct mg_ppo_config {
     uint32_t minibatch;
     uint32_t seed;
     float lr;
-    uint32_t reserved;
+    /* MG_PRECISION_FP32 (default), or MG_PRECISION_BF16: the policy forward
+     * multiplies bfloat16 operands (weights, LN outputs, hidden activations)
+     * with fp32 accumulation, as the reference's matmuls do; master weights,
+     * Adam and everything else stay fp32 (no reference counterpart as a
+     * switch: the reference is bf16-only, README.md:174-175). */
+    uint32_t precision;
 } mg_ppo_config;
 
 /* Public hyperparameter fields (model/ppo.h:186-191), read on every call. */

@@ -11,7 +11,7 @@
 // step the RNG order is: sample draw(s), reset draws if done, then step
 // (model/ppo.h:728-730, rollout.h:46-47).
 #pragma once
-#include "policy.h"
+#include "policy_bf16.h"
 #include "sample.h"
 
 namespace mg {
@@ -30,14 +30,15 @@ struct CollectShape {
     static constexpr int MIN_WG = M == 16 || O > 32 ? 1 : 2;  // workgroups per CU
 };
 
-template <int M, int O, int HD>
+template <int M, int O, int HD, bool BF16>
 struct CollectSmem {
-    FwdSmem<M> fwd;
+    typename std::conditional<BF16, FwdSmemB<M>, FwdSmem<M>>::type fwd;
     float obs[M * O];
     float head[M * HD];
 };
 
-template <typename Env, int M>
+// BF16: the policy forward multiplies bfloat16 operands (policy_bf16.h).
+template <typename Env, int M, bool BF16>
 __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectShape<M, Env::OBS_DIM>::MIN_WG))
     collect_kernel(const mg_collect_args a) {
     using Tr = EnvTraits<Env>;
@@ -46,7 +47,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     using Obs = typename Env::Obs;
     using CS = CollectShape<M, Env::OBS_DIM>;
     constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
-    __shared__ CollectSmem<M, O, HD> sm;
+    __shared__ CollectSmem<M, O, HD, BF16> sm;
     FwdRegs<M, CS::W> R;
 
     const int tid = threadIdx.x;
@@ -94,7 +95,10 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     __syncthreads();
 
     for (uint32_t t = 0; t <= T; ++t) {
-        policy_forward<M, CS::W>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
+        if constexpr (BF16)
+            policy_forward_b<M, CS::W>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
+        else
+            policy_forward<M, CS::W>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
         if (envLane) {
             const float* h = sm.head + tid * HD;
             if (t == T) {  // bootstrap head for GAE and headValue()
@@ -134,6 +138,25 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     }
 }
 
+template <typename Env, bool BF16>
+int launch_collect_tiles(const mg_collect_args* a) {
+    hipStream_t st = static_cast<hipStream_t>(a->stream);
+    // 64-row tiles reuse each weight fragment across the most rows; they need
+    // n / 64 >= 512 workgroups (2 per CU) to fill the chip. Smaller runs use
+    // 32-row, then 16-row tiles for more workgroups.
+    if (a->n >= 64u * 512u) {
+        hipLaunchKernelGGL((collect_kernel<Env, 64, BF16>), dim3(a->n / 64), dim3(CollectShape<64, Env::OBS_DIM>::NT),
+                           0, st, *a);
+    } else if (a->n >= 32u * 256u) {
+        hipLaunchKernelGGL((collect_kernel<Env, 32, BF16>), dim3(a->n / 32), dim3(CollectShape<32, Env::OBS_DIM>::NT),
+                           0, st, *a);
+    } else {
+        hipLaunchKernelGGL((collect_kernel<Env, 16, BF16>), dim3(a->n / 16), dim3(CollectShape<16, Env::OBS_DIM>::NT),
+                           0, st, *a);
+    }
+    return (int)hipGetLastError();
+}
+
 template <typename Env>
 int launch_collect(const mg_collect_args* a) {
     if (!a || a->n == 0 || a->n % 64 != 0 || a->horizon == 0) return MG_ERR_INVALID;
@@ -141,18 +164,10 @@ int launch_collect(const mg_collect_args* a) {
         a->policy.embed != (uint32_t)kEmbed || a->policy.hidden % kChunk != 0 || a->policy.layers == 0 ||
         a->policy.layers > MG_MAX_LAYERS)
         return MG_ERR_INVALID;
-    hipStream_t st = static_cast<hipStream_t>(a->stream);
-    // 64-row tiles reuse each weight fragment across the most rows; they need
-    // n / 64 >= 512 workgroups (2 per CU) to fill the chip. Smaller runs use
-    // 32-row, then 16-row tiles for more workgroups.
-    if (a->n >= 64u * 512u) {
-        hipLaunchKernelGGL((collect_kernel<Env, 64>), dim3(a->n / 64), dim3(CollectShape<64, Env::OBS_DIM>::NT), 0, st, *a);
-    } else if (a->n >= 32u * 256u) {
-        hipLaunchKernelGGL((collect_kernel<Env, 32>), dim3(a->n / 32), dim3(CollectShape<32, Env::OBS_DIM>::NT), 0, st, *a);
-    } else {
-        hipLaunchKernelGGL((collect_kernel<Env, 16>), dim3(a->n / 16), dim3(CollectShape<16, Env::OBS_DIM>::NT), 0, st, *a);
-    }
-    return (int)hipGetLastError();
+    if (a->policy.precision == MG_PRECISION_BF16 && (!a->policy.frag_fwd32_bf || !a->policy.frag_fwd16_bf))
+        return MG_ERR_INVALID;
+    return a->policy.precision == MG_PRECISION_BF16 ? launch_collect_tiles<Env, true>(a)
+                                                      : launch_collect_tiles<Env, false>(a);
 }
 
 }  // namespace dev

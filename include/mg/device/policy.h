@@ -21,6 +21,7 @@
 // W[g*4KS + 4q + j][n]. Every k is covered once; only the fp32 summation order
 // differs from a sequential loop.
 #pragma once
+#include "../bf16.h"
 #include "common.h"
 
 namespace mg {
@@ -317,11 +318,14 @@ __device__ __forceinline__ void fwd_embed(const float* Win, const float* bias, c
 // model/layernorm.metal:10-71 on the register tile; the result goes to sm.xs.
 // If xn_out/sd_out/x_out are given, the normalised values, the standard
 // deviation and the output are also written there ([M][128], [M], [M][128],
-// row-major; global memory or LDS) for the backward pass.
-template <int M, int W = 4, int NV = 1>
-__device__ __forceinline__ void fwd_layernorm(FwdSmem<M, NV>& sm, const FwdRegs<M, W>& R, const float* gamma,
+// row-major; global memory or LDS) for the backward pass; if xb_out is given,
+// the output rounded to bfloat16 goes there too ([M] rows of stride kLdsB).
+// Smem is any shared-memory layout with an fp32 xs tile.
+constexpr int kLdsB = kEmbed + 8;  // LDS row stride of a bfloat16 tile (elements)
+template <int M, int W = 4, class Smem>
+__device__ __forceinline__ void fwd_layernorm(Smem& sm, const FwdRegs<M, W>& R, const float* gamma,
                                               const float* beta, float* xn_out = nullptr, float* sd_out = nullptr,
-                                              float* x_out = nullptr) {
+                                              float* x_out = nullptr, uint16_t* xb_out = nullptr) {
     constexpr int TPR = Shape<M, W>::NT / M;  // threads per row
     constexpr int CPT = kEmbed / TPR;         // columns per thread
     static_assert(CPT % 4 == 0, "float4 columns");
@@ -362,6 +366,11 @@ __device__ __forceinline__ void fwd_layernorm(FwdSmem<M, NV>& sm, const FwdRegs<
         *reinterpret_cast<f32x4*>(xr + c) = o;
         if (xn_out) *reinterpret_cast<f32x4*>(xn_out + row * kEmbed + c0 + c) = xn;
         if (x_out) *reinterpret_cast<f32x4*>(x_out + row * kEmbed + c0 + c) = o;
+        if (xb_out) {
+            const uint32_t lo = (uint32_t)bf16_rne(o[0]) | ((uint32_t)bf16_rne(o[1]) << 16);
+            const uint32_t hi = (uint32_t)bf16_rne(o[2]) | ((uint32_t)bf16_rne(o[3]) << 16);
+            *reinterpret_cast<uint2*>(xb_out + row * kLdsB + c0 + c) = make_uint2(lo, hi);
+        }
     }
     if (sd_out && part == 0) sd_out[row] = sd;
     __syncthreads();
@@ -414,8 +423,8 @@ __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSm
 // model/linear.metal:17-37: head[row][j] = sum_k xs[row][k] W_head[k][j] for
 // j < HD, into headL ([M][HD] in LDS). Wh is W_head ([128][HD], global memory
 // or LDS). Ends with a barrier.
-template <int M, int W = 4, int NV = 1>
-__device__ __forceinline__ void fwd_head(const float* Wh, FwdSmem<M, NV>& sm, float* headL, int HD) {
+template <int M, int W = 4, class Smem>
+__device__ __forceinline__ void fwd_head(const float* Wh, Smem& sm, float* headL, int HD) {
     constexpr int TPR = Shape<M, W>::NT / M, CPT = kEmbed / TPR;
     const int tid = threadIdx.x, row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     const float* wp = Wh + c0 * HD;

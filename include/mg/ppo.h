@@ -50,8 +50,10 @@ struct PPOModel {
 
     // model/ppo.h:274. minibatch: rows per PPO minibatch (multiple of 64 dividing
     // the env count; 0 = min(envs, 4096), which is one whole slot at 4096 envs).
+    // precision: MG_PRECISION_FP32, or MG_PRECISION_BF16 for bfloat16 matrix
+    // operands in the policy forward (the reference's matmul precision).
     PPOModel(Gym<Env>& g, int e, int s, int layers, float learningRate, int T = 32, uint32_t seed = 0,
-             uint32_t minibatch = 0)
+             uint32_t minibatch = 0, uint32_t precision = MG_PRECISION_FP32)
         : gym(g), parallels(g.parallels), horizon((uint32_t)(T > 0 ? T : 0)) {
         mg_ppo_config cfg{};
         cfg.embed = (uint32_t)e;
@@ -61,6 +63,7 @@ struct PPOModel {
         cfg.minibatch = minibatch;
         cfg.seed = seed;
         cfg.lr = learningRate;
+        cfg.precision = precision;
         if (mg_ppo_check_config(Env::KERNEL, parallels, &cfg) != MG_OK) {  // model/ppo.h:290-298
             std::cerr << mg_last_error() << "\n";
             std::exit(1);

@@ -31,8 +31,10 @@ class EnvDesc(C.Structure):
 
 
 class PolicyView(C.Structure):
-    _fields_ = [("params", P), ("frag_fwd32", P), ("frag_fwd16", P), ("frag_bwd16", P)] + [(n, u32) for n in ("obs_dim", "act_dim", "embed", "hidden", "layers", "head_dim",
-                                                       "continuous", "count", "off_in_w", "off_in_b")] + [
+    _fields_ = [(n, P) for n in ("params", "frag_fwd32", "frag_fwd16", "frag_bwd16", "frag_fwd32_bf",
+                                 "frag_fwd16_bf")] + [(n, u32) for n in (
+        "obs_dim", "act_dim", "embed", "hidden", "layers", "head_dim", "continuous", "precision", "count", "off_in_w",
+        "off_in_b")] + [
         ("off_ln_gamma", u32 * (MAX_LAYERS + 1)),
         ("off_ln_beta", u32 * (MAX_LAYERS + 1)),
         ("off_up", u32 * MAX_LAYERS),
@@ -50,7 +52,7 @@ class GymBuffers(C.Structure):
 
 class PPOConfig(C.Structure):
     _fields_ = [(n, u32) for n in ("embed", "scale", "layers", "horizon", "minibatch", "seed")] + [("lr", f32),
-                                                                                                    ("reserved", u32)]
+                                                                                                    ("precision", u32)]
 
 
 class PPOHParams(C.Structure):
@@ -334,9 +336,10 @@ class Gym:
 class PPOModel:
     """mg_ppo_* (model/ppo.h:106-1009)."""
 
-    def __init__(self, gym: Gym, embed=128, scale=4, layers=2, lr=3e-4, horizon=32, seed=0, minibatch=0):
+    def __init__(self, gym: Gym, embed=128, scale=4, layers=2, lr=3e-4, horizon=32, seed=0, minibatch=0,
+                 precision="fp32"):
         self.gym = gym
-        cfg = PPOConfig(embed, scale, layers, horizon, minibatch, seed, lr, 0)
+        cfg = PPOConfig(embed, scale, layers, horizon, minibatch, seed, lr, {"fp32": 0, "bf16": 1}[precision])
         h = C.c_void_p()
         check(lib().mg_ppo_create(gym.h, C.byref(cfg), C.byref(h)))
         self.h = h.value

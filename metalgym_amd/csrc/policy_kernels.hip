@@ -2,7 +2,7 @@
 // per-row sampling (act() and teacher-forced parity), GAE and the per-block
 // advantage statistics used by the PPO loss.
 #include "kernels.h"
-#include "mg/device/policy.h"
+#include "mg/device/policy_bf16.h"
 #include "mg/device/sample.h"
 
 namespace mg {
@@ -13,10 +13,10 @@ constexpr int kMaxHead = 64;  // ACT_DIM + 1 limit (model/ppo.h:117)
 
 // model/ppo.h:575-626 on `rows` obs rows; rows past the end compute on zeros
 // and are not stored.
-template <int M>
+template <int M, bool BF16>
 __global__ void __launch_bounds__(256) forward_kernel(const mg_policy_view pv, const float* __restrict__ obs,
                                                       uint32_t rows, float* __restrict__ head) {
-    __shared__ FwdSmem<M> sm;
+    __shared__ typename std::conditional<BF16, FwdSmemB<M>, FwdSmem<M>>::type sm;
     __shared__ float obsL[M * kMaxObs];
     __shared__ float headL[M * kMaxHead];
     FwdRegs<M> R;
@@ -27,7 +27,10 @@ __global__ void __launch_bounds__(256) forward_kernel(const mg_policy_view pv, c
         obsL[idx] = r < rows ? obs[(size_t)row0 * O + idx] : 0.0f;
     }
     __syncthreads();
-    policy_forward<M>(pv, sm, R, obsL, O, headL, HD);
+    if constexpr (BF16)
+        policy_forward_b<M>(pv, sm, R, obsL, O, headL, HD);
+    else
+        policy_forward<M>(pv, sm, R, obsL, O, headL, HD);
     for (int idx = threadIdx.x; idx < M * HD; idx += 256) {
         const uint32_t r = row0 + idx / HD;
         if (r < rows) head[(size_t)row0 * HD + idx] = headL[idx];
@@ -140,7 +143,12 @@ int launch_forward(hipStream_t st, const mg_policy_view& pv, const float* obs, u
     MG_CHECK(pv.obs_dim <= (uint32_t)dev::kMaxObs && pv.head_dim <= (uint32_t)dev::kMaxHead, MG_ERR_INVALID,
              "forward: OBS_DIM must be <= %d and ACT_DIM + 1 <= %d", dev::kMaxObs, dev::kMaxHead);
     if (rows == 0) return MG_OK;
-    hipLaunchKernelGGL((dev::forward_kernel<32>), dim3((rows + 31) / 32), dim3(256), 0, st, pv, obs, rows, head);
+    if (pv.precision == MG_PRECISION_BF16)
+        hipLaunchKernelGGL((dev::forward_kernel<32, true>), dim3((rows + 31) / 32), dim3(256), 0, st, pv, obs, rows,
+                           head);
+    else
+        hipLaunchKernelGGL((dev::forward_kernel<32, false>), dim3((rows + 31) / 32), dim3(256), 0, st, pv, obs, rows,
+                           head);
     MG_HIP(hipGetLastError(), "forward launch");
     return MG_OK;
 }

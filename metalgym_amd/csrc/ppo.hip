@@ -199,6 +199,8 @@ int validate_config(const mg_env_desc* env, uint32_t n, const mg_ppo_config* c, 
     MG_CHECK(c->layers >= 1 && c->layers <= MG_MAX_LAYERS, MG_ERR_INVALID, "PPOModel: layers %u must be in [1, %d]",
              c->layers, MG_MAX_LAYERS);
     MG_CHECK(c->horizon >= 1, MG_ERR_INVALID, "PPOModel: horizon must be >= 1");
+    MG_CHECK(c->precision == MG_PRECISION_FP32 || c->precision == MG_PRECISION_BF16, MG_ERR_INVALID,
+             "PPOModel: precision %u must be MG_PRECISION_FP32 or MG_PRECISION_BF16", c->precision);
     MG_CHECK(env->obs_dim >= 1 && env->obs_dim <= 64, MG_ERR_INVALID, "PPOModel: OBS_DIM %u must be in [1, 64]",
              env->obs_dim);
     MG_CHECK(env->act_dim >= 1 && env->act_dim + 1 <= 64, MG_ERR_INVALID,
@@ -247,6 +249,7 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
     pv.hidden = c->embed * c->scale;
     pv.layers = c->layers;
     pv.continuous = env->continuous;
+    pv.precision = c->precision;
     make_layout(pv);
     auto fail = [&](int code) {
         mg_ppo_destroy(p);
@@ -260,6 +263,9 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
         (rc = device_alloc((void**)&pv.frag_fwd32, (size_t)pv.count * 4, "PPOModel forward matrix tiles")) ||
         (rc = device_alloc((void**)&pv.frag_fwd16, (size_t)pv.count * 4, "PPOModel forward matrix tiles")) ||
         (rc = device_alloc((void**)&pv.frag_bwd16, (size_t)pv.count * 4, "PPOModel backward matrix tiles")) ||
+        (pv.precision == MG_PRECISION_BF16 &&
+         ((rc = device_alloc((void**)&pv.frag_fwd32_bf, (size_t)pv.count * 2, "PPOModel bf16 matrix tiles")) ||
+          (rc = device_alloc((void**)&pv.frag_fwd16_bf, (size_t)pv.count * 2, "PPOModel bf16 matrix tiles")))) ||
         (rc = device_alloc((void**)&p->m, (size_t)pv.count * 4, "PPOModel adam m")) ||
         (rc = device_alloc((void**)&p->v, (size_t)pv.count * 4, "PPOModel adam v")) ||
         (rc = device_alloc((void**)&p->obs_slots, (T + 1) * n * env->obs_dim * 4, "obs slots")) ||
@@ -290,7 +296,9 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
         hipMemsetAsync(p->head, 0, (size_t)p->head_cap * pv.head_dim * 4, st) != hipSuccess ||
         hipMemsetAsync(pv.frag_fwd32, 0, (size_t)pv.count * 4, st) != hipSuccess ||
         hipMemsetAsync(pv.frag_fwd16, 0, (size_t)pv.count * 4, st) != hipSuccess ||
-        hipMemsetAsync(pv.frag_bwd16, 0, (size_t)pv.count * 4, st) != hipSuccess)
+        hipMemsetAsync(pv.frag_bwd16, 0, (size_t)pv.count * 4, st) != hipSuccess ||
+        (pv.frag_fwd32_bf && hipMemsetAsync(pv.frag_fwd32_bf, 0, (size_t)pv.count * 2, st) != hipSuccess) ||
+        (pv.frag_fwd16_bf && hipMemsetAsync(pv.frag_fwd16_bf, 0, (size_t)pv.count * 2, st) != hipSuccess))
         return fail(set_error(MG_ERR_HIP, "PPOModel: initialisation upload failed"));
     if ((rc = launch_derive_blocks(st, pv))) return fail(rc);
     if (hipStreamSynchronize(st) != hipSuccess)
@@ -309,6 +317,8 @@ int mg_ppo_destroy(mg_ppo* p) {
     (void)hipFree(p->pv.frag_fwd32);
     (void)hipFree(p->pv.frag_fwd16);
     (void)hipFree(p->pv.frag_bwd16);
+    (void)hipFree(p->pv.frag_fwd32_bf);
+    (void)hipFree(p->pv.frag_fwd16_bf);
     (void)hipFree(p->m);
     (void)hipFree(p->v);
     (void)hipFree(p->obs_slots);

@@ -21,7 +21,7 @@
 #include <string.h>
 
 #include "kernels.h"
-#include "mg/device/policy.h"
+#include "mg/device/policy_bf16.h"
 #include "mg/device/sample.h"
 
 namespace mg {
@@ -596,13 +596,26 @@ __device__ __forceinline__ MatTile mat_tile(uint32_t t, uint32_t float_group, ui
 }
 constexpr int kTileLd = kTT + 1;  // LDS row stride of such a tile
 
+// Packs lds[(k0 + i) * kTileLd + n], i = 0..7, as eight bf16 (16 bytes).
+__device__ __forceinline__ u32x4 pack_bf16_column(const float* lds, int k0, int n) {
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)bf16_rne(lds[(k0 + 2 * j) * kTileLd + n]) |
+               ((uint32_t)bf16_rne(lds[(k0 + 2 * j + 1) * kTileLd + n]) << 16);
+    return w;
+}
+
 // Writes the tile held in lds ([r][c], stride kTileLd) to the fragment-tiled
 // copies: frag_fwd32 and frag_fwd16 read its transpose (rows n = c,
 // contraction k = r, K = rows), frag_bwd16 the matrix as stored (n = r, k = c,
 // K = cols). Each thread writes one float4 (four consecutive k of one n) to
-// each; a wave's 64 float4s form one 1 KB run. Starts with a barrier.
+// each; a wave's 64 float4s form one 1 KB run. The bf16 copies of the
+// transpose (when given) take 8 k per thread: threads 0-127 the 32-wide strip
+// (two k-groups of 16), threads 128-255 the two 16-wide strips (one k-group of
+// 32). Starts with a barrier.
 __device__ __forceinline__ void store_tile_frags(const MatTile& m, const float* lds, float* fwd32, float* fwd16,
-                                                 float* bwd16) {
+                                                 float* bwd16, uint16_t* fwd32b, uint16_t* fwd16b) {
     __syncthreads();
     const int t = threadIdx.x;
     {  // 32-wide strips: the tile is one strip's four k-groups, 4 KB in a row
@@ -621,12 +634,24 @@ __device__ __forceinline__ void store_tile_frags(const MatTile& m, const float* 
     }
     *reinterpret_cast<f32x4*>(bwd16 + m.base + frag_index<16>(m.r0 + n, m.c0 + k, m.cols)) = vb;
     *reinterpret_cast<f32x4*>(fwd16 + m.base + frag_index<16>(m.c0 + n, m.r0 + k, m.rows)) = vf;
+    if (fwd32b) {
+        if (t < 128) {
+            const int ln = t & 63, nb = ln & 31, kb = 16 * (t >> 6) + 8 * (ln >> 5);
+            *reinterpret_cast<u32x4*>(fwd32b + m.base + frag_index_b<32>(m.c0 + nb, m.r0 + kb, m.rows)) =
+                pack_bf16_column(lds, kb, nb);
+        } else {
+            const int t2 = t - 128, ln = t2 & 63, nb = 16 * (t2 >> 6) + (ln & 15), kb = 8 * (ln >> 4);
+            *reinterpret_cast<u32x4*>(fwd16b + m.base + frag_index_b<16>(m.c0 + nb, m.r0 + kb, m.rows)) =
+                pack_bf16_column(lds, kb, nb);
+        }
+    }
 }
 
 // The fragment-tiled copies from params, one tile per workgroup.
 __global__ void __launch_bounds__(256) derive_blocks_kernel(const float* __restrict__ param, float* __restrict__ fwd32,
                                                             float* __restrict__ fwd16, float* __restrict__ bwd16,
-                                                            uint32_t float_group, uint32_t H) {
+                                                            uint16_t* fwd32b, uint16_t* fwd16b, uint32_t float_group,
+                                                            uint32_t H) {
     __shared__ float lds[kTT * kTileLd];
     const MatTile m = mat_tile(blockIdx.x, float_group, H);
     const int t = threadIdx.x, c = t & (kTT - 1);
@@ -635,7 +660,7 @@ __global__ void __launch_bounds__(256) derive_blocks_kernel(const float* __restr
         const int r = (256 / kTT) * e + t / kTT;
         lds[r * kTileLd + c] = param[m.base + (size_t)(m.r0 + r) * m.cols + m.c0 + c];
     }
-    store_tile_frags(m, lds, fwd32, fwd16, bwd16);
+    store_tile_frags(m, lds, fwd32, fwd16, bwd16, fwd32b, fwd16b);
 }
 
 struct AdamArgs {
@@ -643,6 +668,8 @@ struct AdamArgs {
     float* frag_fwd32;
     float* frag_fwd16;
     float* frag_bwd16;
+    uint16_t* frag_fwd32_bf;
+    uint16_t* frag_fwd16_bf;
     const float* grad;
     float* mom;
     float* var;
@@ -713,7 +740,7 @@ __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
             const int r = (256 / kTT) * e + t / kTT;
             lds[r * kTileLd + c] = adam_elem(a, idx[e], in[e], scale);
         }
-        store_tile_frags(m, lds, a.frag_fwd32, a.frag_fwd16, a.frag_bwd16);
+        store_tile_frags(m, lds, a.frag_fwd32, a.frag_fwd16, a.frag_bwd16, a.frag_fwd32_bf, a.frag_fwd16_bf);
         return;
     }
     const uint32_t j = (blockIdx.x - a.mat_tiles) * 256 + t;
@@ -796,7 +823,7 @@ int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv) {
     int rc = check_matrix_layout(pv);
     if (rc) return rc;
     hipLaunchKernelGGL(dev::derive_blocks_kernel, dim3(mat_tiles(pv)), dim3(256), 0, st, pv.params, pv.frag_fwd32,
-                       pv.frag_fwd16, pv.frag_bwd16, pv.float_group, pv.hidden);
+                       pv.frag_fwd16, pv.frag_bwd16, pv.frag_fwd32_bf, pv.frag_fwd16_bf, pv.float_group, pv.hidden);
     MG_HIP(hipGetLastError(), "derive blocks launch");
     return MG_OK;
 }
@@ -885,6 +912,8 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         aa.frag_fwd32 = pv.frag_fwd32;
         aa.frag_fwd16 = pv.frag_fwd16;
         aa.frag_bwd16 = pv.frag_bwd16;
+        aa.frag_fwd32_bf = pv.frag_fwd32_bf;
+        aa.frag_fwd16_bf = pv.frag_fwd16_bf;
         aa.grad = ws.grad;
         aa.mom = m;
         aa.var = v;

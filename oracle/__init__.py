@@ -30,7 +30,7 @@ class EnvInfo(C.Structure):
 
 
 class Dims(C.Structure):
-    _fields_ = [(n, C.c_uint32) for n in ("obs_dim", "act_dim", "embed", "hidden", "layers", "continuous")]
+    _fields_ = [(n, C.c_uint32) for n in ("obs_dim", "act_dim", "embed", "hidden", "layers", "continuous", "bf16")]
 
 
 class Layout(C.Structure):
@@ -86,6 +86,7 @@ def lib():
             "orc_env_reset": (None, [C.c_int, P, P]),
             "orc_env_step": (None, [C.c_int, P, P, P, P, P]),
             "orc_rollout": (None, [C.c_int, u32, u32, C.c_int, P, P, P, P, P, P, P, P, C.c_int]),
+            "orc_round_bf16": (f32, [f32]),
             "orc_expf": (f32, [f32]),
             "orc_logf": (f32, [f32]),
             "orc_sinf": (f32, [f32]),
@@ -125,9 +126,9 @@ def env_info(env: int) -> EnvInfo:
     return info
 
 
-def dims(env: int, hidden: int = 512, layers: int = 2, embed: int = 128) -> Dims:
+def dims(env: int, hidden: int = 512, layers: int = 2, embed: int = 128, bf16: bool = False) -> Dims:
     i = env_info(env)
-    return Dims(i.obs_dim, i.act_dim, embed, hidden, layers, i.continuous)
+    return Dims(i.obs_dim, i.act_dim, embed, hidden, layers, i.continuous, 1 if bf16 else 0)
 
 
 def layout(d: Dims) -> Layout:

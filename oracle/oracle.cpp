@@ -448,6 +448,18 @@ void ln_forward(const float* h, const float* gamma, const float* beta, uint32_t 
     }
 }
 
+// bfloat16 rounding of an fp32 value (round to nearest, ties to even), kept as
+// the float it represents: the matrix operands of the reference's matmuls
+// (model/mlp.metal:43-48, 80-85 multiply bfloat16 tiles).
+float round_bf16(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+    float r;
+    std::memcpy(&r, &u, 4);
+    return r;
+}
+
 // Per-row activation record for the backward pass.
 struct Acts {
     std::vector<float> xn, x, sd, v;  // xn/x: [(L+1)][E], sd: [L+1], v: [L][H]
@@ -475,23 +487,31 @@ void forward_row(const Net& n, const float* obs, float* head, float* xn_out, flo
         if (xn_out) std::memcpy(xn_out + l * E, xn.data(), E * 4);
         if (x_out) std::memcpy(x_out + l * E, x.data(), E * 4);
         if (sd_out) sd_out[l] = sd;
-        // model/mlp.metal:18-58: V = X Up, relu
+        // model/mlp.metal:18-58: V = X Up, relu (bf16 operands: X and Up rounded)
         const float* Up = n.P + n.L.off_up[l];
+        const bool bf = n.d.bf16 != 0;
         std::fill(v.begin(), v.end(), 0.0f);
         for (uint32_t k = 0; k < E; ++k) {
-            float xk = x[k];
+            float xk = bf ? round_bf16(x[k]) : x[k];
             const float* row = Up + (size_t)k * H;
-            for (uint32_t j = 0; j < H; ++j) v[j] += xk * row[j];
+            if (bf)
+                for (uint32_t j = 0; j < H; ++j) v[j] += xk * round_bf16(row[j]);
+            else
+                for (uint32_t j = 0; j < H; ++j) v[j] += xk * row[j];
         }
         for (uint32_t j = 0; j < H; ++j) v[j] = v[j] > 0.0f ? v[j] : 0.0f;
         if (v_out) std::memcpy(v_out + (size_t)l * H, v.data(), H * 4);
-        // model/mlp.metal:60-86: Out = V Down; model/elementwise.metal:4-13 residual add
+        // model/mlp.metal:60-86: Out = V Down (bf16 operands: V and Down rounded);
+        // model/elementwise.metal:4-13 residual add
         const float* Dn = n.P + n.L.off_down[l];
         std::fill(out.begin(), out.end(), 0.0f);
         for (uint32_t j = 0; j < H; ++j) {
-            float vj = v[j];
+            float vj = bf ? round_bf16(v[j]) : v[j];
             const float* row = Dn + (size_t)j * E;
-            for (uint32_t c = 0; c < E; ++c) out[c] += vj * row[c];
+            if (bf)
+                for (uint32_t c = 0; c < E; ++c) out[c] += vj * round_bf16(row[c]);
+            else
+                for (uint32_t c = 0; c < E; ++c) out[c] += vj * row[c];
         }
         for (uint32_t c = 0; c < E; ++c) h[c] = h[c] + out[c];
     }
@@ -596,6 +616,7 @@ float orc_rng_uniform(uint32_t* s) { return xs_unif(*s); }
 float orc_rng_uniform_range(uint32_t* s, float lo, float hi) { return xs_unif(*s, lo, hi); }
 uint32_t orc_rng_int(uint32_t* s, uint32_t n) { return xs_next(*s) % n; }
 
+float orc_round_bf16(float x) { return round_bf16(x); }
 float orc_expf(float x) { return mg::expf(x); }
 float orc_logf(float x) { return mg::logf(x); }
 float orc_sinf(float x) { return mg::sinf(x); }

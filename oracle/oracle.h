@@ -36,6 +36,7 @@ typedef struct orc_dims {
     uint32_t hidden;
     uint32_t layers;
     uint32_t continuous;
+    uint32_t bf16; /* 1: the block GEMMs of the forward take bfloat16 operands */
 } orc_dims;
 
 typedef struct orc_layout {
@@ -74,6 +75,7 @@ void orc_rollout(int env, uint32_t n, uint32_t steps, int random, void* state, u
                  int threads);
 
 /* math shared with the product (include/mg/math.h), exported for pinning tests */
+float orc_round_bf16(float x); /* bfloat16 rounding (nearest, ties to even) */
 float orc_expf(float x);
 float orc_logf(float x);
 float orc_sinf(float x);

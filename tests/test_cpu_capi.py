@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported(mg):
 
 
 def test_abi_version(mg):
-    assert mg.lib().mg_abi_version() == 3
+    assert mg.lib().mg_abi_version() == 4
 
 
 def test_builtin_envs_registered(mg):
@@ -69,7 +69,7 @@ def test_gym_rejects_zero_envs(mg):
 
 
 def cfg(**kw):
-    base = dict(embed=128, scale=4, layers=2, horizon=32, minibatch=0, seed=0, lr=3e-4, reserved=0)
+    base = dict(embed=128, scale=4, layers=2, horizon=32, minibatch=0, seed=0, lr=3e-4, precision=0)
     base.update(kw)
     return PPOConfig(**base)
 

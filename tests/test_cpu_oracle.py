@@ -359,3 +359,51 @@ def test_voxelnav_reset_and_step_spec(orc):
             if d[0]:
                 break
     assert abs(np.mean(occ) - 0.25) < 0.02
+
+
+def test_bf16_rounding_matches_torch(orc):
+    """The oracle's bfloat16 rounding against torch's float -> bfloat16 cast
+    (round to nearest, ties to even), including exact ties either side."""
+    import torch
+
+    rs = np.random.default_rng(21)
+    x = (rs.standard_normal(20000) * np.exp(rs.uniform(-20, 20, 20000))).astype(np.float32)
+    ties = (rs.integers(1, 2**31, 2000, dtype=np.int64).astype(np.uint32) & 0xFFFF0000) | 0x8000
+    x = np.concatenate([x, ties.view(np.float32), np.float32([0.0, -0.0, 1.0, 65504.0, 1e-38])])
+    x = x[np.isfinite(x)]  # the rounding is defined for finite values
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = np.array([orc.lib().orc_round_bf16(float(v)) for v in x], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["ppo_categorical", "ppo_voxel_shape"])
+def test_bf16_forward_vs_torch(orc, name):
+    """The bf16 forward: the block GEMMs' operands (LN output, up and down
+    weights, relu'd hidden) rounded to bfloat16 from their fp32 values, all else
+    as the fp32 forward, against a float64 torch forward with the same operand
+    rounding. The fp32 forward differs from it by much more than the bound, so
+    a dropped rounding point fails."""
+    import torch
+    import torch.nn.functional as F
+
+    from golden import make_golden as mk
+
+    z = load(name)
+    O, A, E, H, L, cont, B = (int(x) for x in z["dims"])
+    d = orc.Dims(O, A, E, H, L, cont, 1)
+    head = orc.forward(d, z["params0"], z["obs"], threads=2)
+    t = mk.torch_params(z["params0"], O, A, E, H, L, bool(cont))
+    bf = lambda v: v.float().to(torch.bfloat16).double()
+    with torch.no_grad():
+        h = torch.tensor(z["obs"], dtype=torch.float64) @ t["in_w"] + t["in_b"]
+        for l in range(L):
+            x = F.layer_norm(h, (E,), t[f"g{l}"], t[f"b{l}"], eps=1e-5)
+            v = torch.relu(bf(x) @ bf(t[f"up{l}"]))
+            h = h + bf(v) @ bf(t[f"down{l}"])
+        x = F.layer_norm(h, (E,), t[f"g{L}"], t[f"b{L}"], eps=1e-5)
+        want = (x @ t["head"]).numpy()
+    err = np.abs(head - want).max() / max(1.0, np.abs(want).max())
+    fp32 = orc.forward(orc.Dims(O, A, E, H, L, cont, 0), z["params0"], z["obs"], threads=2)
+    gap = np.abs(fp32 - want).max() / max(1.0, np.abs(want).max())
+    assert err < 2e-4, err
+    assert gap > 10 * err, (gap, err)

@@ -5,16 +5,18 @@ resets and done flags must match bit for bit, the policy head and values to
 import numpy as np
 import pytest
 
-from parity import ENVS, THREADS, TOL_HEAD, assert_bit_exact, assert_close
+from parity import ENVS, THREADS, TOL_HEAD, assert_bit_exact, assert_close, assert_close_bf16
 
 pytestmark = pytest.mark.gpu
 
 
-def run_collect_parity(mg, orc, env, n, T, layers=2, scale=4, seed=0, collects=2):
+def run_collect_parity(mg, orc, env, n, T, layers=2, scale=4, seed=0, collects=2, bf16=False):
+    close = (lambda g, w, what: assert_close_bf16(g, w, what)) if bf16 else \
+        (lambda g, w, what: assert_close(g, w, TOL_HEAD, what))
     eid, kernel = ENVS[env]
     gym = mg.Gym(kernel, n, seed)
-    model = mg.PPOModel(gym, scale=scale, layers=layers, horizon=T, seed=seed)
-    d = orc.dims(eid, hidden=128 * scale, layers=layers)
+    model = mg.PPOModel(gym, scale=scale, layers=layers, horizon=T, seed=seed, precision="bf16" if bf16 else "fp32")
+    d = orc.dims(eid, hidden=128 * scale, layers=layers, bf16=bf16)
     params = orc.init_params(d, seed)
     assert_bit_exact(model.params(), params, "initial parameters")
     g = orc.GymState(eid, n, seed)
@@ -33,20 +35,20 @@ def run_collect_parity(mg, orc, env, n, T, layers=2, scale=4, seed=0, collects=2
         assert_bit_exact(gym.rng(), g.rng, f"{tag} rng")
         assert_bit_exact(gym.state(), g.state, f"{tag} state")
         assert_bit_exact(gym.done(), g.done, f"{tag} live done")
-        # policy side: within 1e-4
-        assert_close(s["value"], slots.value, TOL_HEAD, f"{tag} values")
-        assert_close(s["logp"], slots.logp, TOL_HEAD, f"{tag} logp")
-        assert_close(head, slots.head, TOL_HEAD, f"{tag} bootstrap head")
+        # policy side: within 1e-4 (bf16: in bulk, with bounded flipped rows)
+        close(s["value"], slots.value, f"{tag} values")
+        close(s["logp"], slots.logp, f"{tag} logp")
+        close(head, slots.head, f"{tag} bootstrap head")
         if gym.continuous:
-            assert_close(s["actions"], sampled, TOL_HEAD, f"{tag} gaussian samples")
+            close(s["actions"], sampled, f"{tag} gaussian samples")
         else:
             flips = int((s["actions"] != sampled).sum())
-            assert flips <= max(2, s["actions"].size // 10000), f"{tag}: {flips} sampled actions differ"
+            assert flips <= max(2, s["actions"].size // (1000 if bf16 else 10000)), f"{tag}: {flips} sampled actions differ"
         # GAE: bit-exact on the GPU's own inputs, 1e-4 against the oracle's
         adv, ret = orc.gae(s["reward"], s["done"], s["value"], head, gym.act_dim)
         assert_bit_exact(s["adv"], adv, f"{tag} advantages")
         assert_bit_exact(s["ret"], ret, f"{tag} returns")
-        assert_close(s["adv"], slots.adv, TOL_HEAD, f"{tag} advantages vs oracle")
+        close(s["adv"], slots.adv, f"{tag} advantages vs oracle")
     return model, s
 
 
