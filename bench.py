@@ -92,11 +92,11 @@ def bench_random(n, T, reps, kernel="rollout_cartpole", hbm=True):
     return out
 
 
-def bench_full(kernel, n, T, iters, O, A, epochs=4):
+def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32"):
     import metalgym_amd as mg
 
     gym = mg.Gym(kernel, n, 0)
-    model = mg.PPOModel(gym, horizon=T)
+    model = mg.PPOModel(gym, horizon=T, precision=precision)
     model.collect()
     model.train(1)
     sync()
@@ -297,6 +297,9 @@ def main():
         _, _, dtb4, _ = bench_collect("rollout_cartpole", 4096, 32, 20, 2, O, A, precision="bf16")
         extra["bf16_collect_4096"] = {"env_steps_per_s": 20 * 4096 * 32 / dtb4,
                                       "vs_published_m4_3.8M": 20 * 4096 * 32 / dtb4 / 3.8e6}
+        extra["bf16_full_ppo_262144"] = bench_full("rollout_cartpole", 262144, 32, 1, O, A, precision="bf16")
+        extra["bf16_full_ppo_4096"] = bench_full("rollout_cartpole", 4096, 32, 5, O, A, precision="bf16")
+        extra["bf16_full_ppo_4096"]["vs_published_m4_296K"] = extra["bf16_full_ppo_4096"]["env_steps_per_s"] / 296e3
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

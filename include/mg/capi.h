@@ -106,10 +106,10 @@ typedef struct mg_rollout_args {
  * matrix's offset (MT = 32, KG = 8 for 32x32x2; MT = 16, KG = 16 for 16x16x4).
  * frag_fwd32 and frag_fwd16 hold up^T and down^T (the forward's operands),
  * frag_bwd16 up and down as stored (the backward's). With precision
- * MG_PRECISION_BF16, frag_fwd32_bf and frag_fwd16_bf hold up^T and down^T
- * rounded to bfloat16 (16-bit patterns) in the operand order of the bf16
- * instructions (32x32x16 and 16x16x32: k-groups of 16 and 32, each lane 8
- * consecutive k); otherwise they are NULL. The library derives all of them
+ * MG_PRECISION_BF16, frag_fwd32_bf and frag_fwd16_bf hold up^T and down^T and
+ * frag_bwd16_bf up and down, rounded to bfloat16 (16-bit patterns), in the
+ * operand order of the bf16 instructions (32x32x16 and 16x16x32: k-groups of
+ * 16 and 32, each lane 8 consecutive k); otherwise they are NULL. The library derives all of them
  * from params at creation, in every Adam step and in mg_ppo_set_params /
  * mg_ppo_params_updated; the fused kernels read the matrices from them. */
 enum { MG_PRECISION_FP32 = 0, MG_PRECISION_BF16 = 1 };
@@ -120,6 +120,7 @@ typedef struct mg_policy_view {
     float* frag_bwd16;
     uint16_t* frag_fwd32_bf;
     uint16_t* frag_fwd16_bf;
+    uint16_t* frag_bwd16_bf;
     uint32_t obs_dim;
     uint32_t act_dim;
     uint32_t embed;
@@ -240,11 +241,12 @@ typedef struct mg_ppo_config {
     uint32_t minibatch;
     uint32_t seed;
     float lr;
-    /* MG_PRECISION_FP32 (default), or MG_PRECISION_BF16: the policy forward
-     * multiplies bfloat16 operands (weights, LN outputs, hidden activations)
+    /* MG_PRECISION_FP32 (default), or MG_PRECISION_BF16: the block matmuls of
+     * the forward, the backward and the weight gradients multiply bfloat16
+     * operands (weights, LN outputs, hidden activations and their gradients)
      * with fp32 accumulation, as the reference's matmuls do; master weights,
-     * Adam and everything else stay fp32 (no reference counterpart as a
-     * switch: the reference is bf16-only, README.md:174-175). */
+     * Adam, LN, head and embed stay fp32 (no reference counterpart as a switch:
+     * the reference is bf16-only, README.md:174-175). */
     uint32_t precision;
 } mg_ppo_config;
 

@@ -50,12 +50,13 @@ __host__ __device__ constexpr uint32_t frag_index_b(uint32_t n, uint32_t k, uint
 }
 
 // LDS of one forward tile: the fp32 LN output (staging, and the head's input
-// after the final LN) and the bf16 GEMM operands.
-template <int M>
+// after the final LN) and the bf16 GEMM operands; NV = 2 double-buffers the
+// hidden chunk (one barrier per chunk).
+template <int M, int NV = 1>
 struct FwdSmemB {
     float xs[M * kLds];
-    uint16_t xb[M * kLdsB];  // LN output of the block's input, bf16
-    uint16_t vb[M * kLdsB];  // relu'd hidden chunk, bf16
+    uint16_t xb[M * kLdsB];      // LN output of the block's input, bf16
+    uint16_t vb[NV][M * kLdsB];  // relu'd hidden chunk, bf16
 };
 
 struct FragSrcB {
@@ -195,31 +196,47 @@ struct FwdSeqB {
     }
 };
 
-// Writes a register tile to a bf16 LDS tile (row stride kLdsB) through relu.
-template <int M, int W = 4>
+// Writes a register tile to a bf16 LDS tile (row stride kLdsB), optionally
+// through relu.
+template <int M, int W = 4, bool RELU = true>
 __device__ __forceinline__ void store_tile_relu_b(const AccTile<M, W>& acc, uint16_t* lds) {
     for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
         const float x = acc[rt][ct][r];
-        lds[row * kLdsB + col] = bf16_rne(x > 0.0f ? x : 0.0f);
+        lds[row * kLdsB + col] = bf16_rne(RELU ? (x > 0.0f ? x : 0.0f) : x);
+    });
+}
+
+// Writes a register tile rounded to bfloat16 (kept as floats) to global
+// memory (global[row * ld + col]), optionally through relu: the captured
+// operand of a bf16 GEMM.
+template <int M, int W = 4, bool RELU = false>
+__device__ __forceinline__ void store_tile_g_b(const AccTile<M, W>& acc, float* global, size_t ld) {
+    for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
+        float x = acc[rt][ct][r];
+        if (RELU) x = x > 0.0f ? x : 0.0f;
+        global[(size_t)row * ld + col] = bf16_to_float(bf16_rne(x));
     });
 }
 
 // One residual block with bf16 GEMM operands: h += relu(xb Up) Down, chunked
-// as in fwd_block; sm.xb holds the block input's LN output in bf16.
-template <int M, int W, class Seq, class Stream>
-__device__ __forceinline__ void fwd_block_b(const mg_policy_view& pv, int l, FwdSmemB<M>& sm, FwdRegs<M, W>& R,
-                                            Stream& ws, Seq seq) {
+// as in fwd_block; sm.xb holds the block input's LN output in bf16. With VOUT
+// the rounded relu'd hidden activations are also written to v_out.
+template <int M, int W, bool VOUT, int NV, class Seq, class Stream>
+__device__ __forceinline__ void fwd_block_b(const mg_policy_view& pv, int l, FwdSmemB<M, NV>& sm,
+                                            FwdRegs<M, W>& R, Stream& ws, float* v_out, Seq seq) {
     using S = Shape<M, W>;
-    const int NC = (int)pv.hidden / kChunk;
+    const int H = (int)pv.hidden, NC = H / kChunk;
     for (int c = 0; c < NC; ++c) {
         const int s = 2 * (l * NC + c);
+        uint16_t* vb = sm.vb[NV == 2 ? (c & 1) : 0];
         typename S::Acc v[S::RT][S::CT];
         zero<M, W>(v);
         ws.template gemm<0>(v, sm.xb, s, seq);
-        __syncthreads();  // every wave is done reading the previous chunk from vb
-        store_tile_relu_b<M, W>(v, sm.vb);
+        if constexpr (VOUT) store_tile_g_b<M, W, true>(v, v_out + kChunk * c, H);
+        if constexpr (NV == 1) __syncthreads();  // every wave is done reading the previous chunk from vb
+        store_tile_relu_b<M, W>(v, vb);
         __syncthreads();
-        ws.template gemm<1>(R.h, sm.vb, s + 1, seq);
+        ws.template gemm<1>(R.h, vb, s + 1, seq);
     }
 }
 
@@ -238,7 +255,7 @@ __device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, FwdSm
     for (uint32_t l = 0; l < pv.layers; ++l) {
         fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l], nullptr, nullptr,
                             nullptr, sm.xb);
-        fwd_block_b<M, W>(pv, (int)l, sm, R, ws, seq);
+        fwd_block_b<M, W, false, 1, Seq>(pv, (int)l, sm, R, ws, nullptr, seq);
     }
     fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[pv.layers], pv.params + pv.off_ln_beta[pv.layers]);
     fwd_head<M, W>(pv.params + pv.off_head, sm, headL, HD);

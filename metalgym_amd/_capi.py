@@ -32,7 +32,7 @@ class EnvDesc(C.Structure):
 
 class PolicyView(C.Structure):
     _fields_ = [(n, P) for n in ("params", "frag_fwd32", "frag_fwd16", "frag_bwd16", "frag_fwd32_bf",
-                                 "frag_fwd16_bf")] + [(n, u32) for n in (
+                                 "frag_fwd16_bf", "frag_bwd16_bf")] + [(n, u32) for n in (
         "obs_dim", "act_dim", "embed", "hidden", "layers", "head_dim", "continuous", "precision", "count", "off_in_w",
         "off_in_b")] + [
         ("off_ln_gamma", u32 * (MAX_LAYERS + 1)),

@@ -265,7 +265,8 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
         (rc = device_alloc((void**)&pv.frag_bwd16, (size_t)pv.count * 4, "PPOModel backward matrix tiles")) ||
         (pv.precision == MG_PRECISION_BF16 &&
          ((rc = device_alloc((void**)&pv.frag_fwd32_bf, (size_t)pv.count * 2, "PPOModel bf16 matrix tiles")) ||
-          (rc = device_alloc((void**)&pv.frag_fwd16_bf, (size_t)pv.count * 2, "PPOModel bf16 matrix tiles")))) ||
+          (rc = device_alloc((void**)&pv.frag_fwd16_bf, (size_t)pv.count * 2, "PPOModel bf16 matrix tiles")) ||
+          (rc = device_alloc((void**)&pv.frag_bwd16_bf, (size_t)pv.count * 2, "PPOModel bf16 matrix tiles")))) ||
         (rc = device_alloc((void**)&p->m, (size_t)pv.count * 4, "PPOModel adam m")) ||
         (rc = device_alloc((void**)&p->v, (size_t)pv.count * 4, "PPOModel adam v")) ||
         (rc = device_alloc((void**)&p->obs_slots, (T + 1) * n * env->obs_dim * 4, "obs slots")) ||
@@ -298,7 +299,8 @@ int mg_ppo_create(mg_gym* gym, const mg_ppo_config* c, mg_ppo** out) {
         hipMemsetAsync(pv.frag_fwd16, 0, (size_t)pv.count * 4, st) != hipSuccess ||
         hipMemsetAsync(pv.frag_bwd16, 0, (size_t)pv.count * 4, st) != hipSuccess ||
         (pv.frag_fwd32_bf && hipMemsetAsync(pv.frag_fwd32_bf, 0, (size_t)pv.count * 2, st) != hipSuccess) ||
-        (pv.frag_fwd16_bf && hipMemsetAsync(pv.frag_fwd16_bf, 0, (size_t)pv.count * 2, st) != hipSuccess))
+        (pv.frag_fwd16_bf && hipMemsetAsync(pv.frag_fwd16_bf, 0, (size_t)pv.count * 2, st) != hipSuccess) ||
+        (pv.frag_bwd16_bf && hipMemsetAsync(pv.frag_bwd16_bf, 0, (size_t)pv.count * 2, st) != hipSuccess))
         return fail(set_error(MG_ERR_HIP, "PPOModel: initialisation upload failed"));
     if ((rc = launch_derive_blocks(st, pv))) return fail(rc);
     if (hipStreamSynchronize(st) != hipSuccess)
@@ -319,6 +321,7 @@ int mg_ppo_destroy(mg_ppo* p) {
     (void)hipFree(p->pv.frag_bwd16);
     (void)hipFree(p->pv.frag_fwd32_bf);
     (void)hipFree(p->pv.frag_fwd16_bf);
+    (void)hipFree(p->pv.frag_bwd16_bf);
     (void)hipFree(p->m);
     (void)hipFree(p->v);
     (void)hipFree(p->obs_slots);

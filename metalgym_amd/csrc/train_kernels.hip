@@ -34,7 +34,8 @@ constexpr int kMaxHeadT = 64;
 constexpr int kMaxObsT = 64;
 using TS = Shape<kTR, kTW>;
 using TRegs = FwdRegs<kTR, kTW>;
-using TSmem = FwdSmem<kTR, 2>;  // double-buffered hidden chunk
+using TSmem = FwdSmem<kTR, 2>;    // double-buffered hidden chunk
+using TSmemB = FwdSmemB<kTR, 2>;  // the same with bf16 GEMM operands
 
 // Per-tile outer-product sums in one pass: out[k * ks + c * cs] =
 // sum_r a[r * lda + k] * b[r * kLds + c] for k < K and the 128 columns c, rows
@@ -101,7 +102,8 @@ __device__ __forceinline__ void bwd_head(const float* Wh, const float* dheadL, i
 // tile's forward captures (LDS). The tile's sums for dgamma (xn * dZ) and
 // dbeta (dZ) go to tp_gamma / tp_beta (the reference adds them with float
 // atomics).
-__device__ __forceinline__ void bwd_layernorm(TSmem& sm, TRegs& G, const float* xn, const float* sd,
+template <class Smem>
+__device__ __forceinline__ void bwd_layernorm(Smem& sm, TRegs& G, const float* xn, const float* sd,
                                               const float* gamma, float* tp_gamma, float* tp_beta, float* scratch) {
     constexpr int TPR = kTNT / kTR, CPT = kEmbed / TPR;
     const int tid = threadIdx.x;
@@ -160,19 +162,61 @@ struct TrainSeq {
     }
 };
 
+// The bf16 copies' sequences (see BwdSeq, TrainSeq): the same offsets in
+// frag_fwd16_bf and frag_bwd16_bf.
+struct BwdSeqB {
+    const mg_policy_view* pv;
+    int nc;
+    __device__ __forceinline__ FragSrcB operator()(int s) const {
+        const int l = (int)pv->layers - 1 - s / (2 * nc), c = (s >> 1) % nc;
+        if ((s & 1) == 0) return {pv->frag_bwd16_bf + pv->off_down[l] + (size_t)kChunk * c * kEmbed, (uint32_t)kEmbed};
+        return {pv->frag_bwd16_bf + pv->off_up[l] + 16 * kChunk * c, pv->hidden};
+    }
+};
+struct TrainSeqB {
+    const mg_policy_view* pv;
+    int nc;
+    __device__ __forceinline__ FragSrcB operator()(int s) const {
+        const int F = 2 * (int)pv->layers * nc;
+        return s < F ? FwdSeqB<16>{pv, nc}(s) : BwdSeqB{pv, nc}(s - F);
+    }
+};
+
+// The row pass's types per precision: LDS tile, weight stream, GEMM sequence.
+template <bool BF>
+struct RowsTypes {
+    using Smem = TSmem;
+    using Stream = TStream<kTR, kTW>;
+    using Seq = TrainSeq;
+};
+template <>
+struct RowsTypes<true> {
+    using Smem = TSmemB;
+    using Stream = TStreamB<kTR, kTW>;
+    using Seq = TrainSeqB;
+};
+
 // Backward of block l (model/mlp.metal:88-153 + model/ppo.h:851-852). D holds
 // the gradient at the block output (dStream) and is updated in place to the
 // gradient at the block input. Chunked like the forward: dV_c = (dh Down_c^T)
 // masked by relu, then dx += dV_c Up_c^T; ws streams the row pass's TrainSeq.
-template <class Stream>
-__device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem& sm, TRegs& D,
+// With BF the two GEMMs take bf16 operands (dh and dV rounded as they are
+// written to LDS; the captures for the weight gradients are the rounded
+// values).
+template <bool BF, class Stream, class Smem>
+__device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, Smem& sm, TRegs& D,
                                           Stream& ws, const float* v_tile, float* dv_store, float* dh_store,
                                           const float* xn_tile, const float* sd_tile, const float* gamma,
                                           float* tp, float* scratch) {
     const int H = (int)pv.hidden, NC = H / kChunk, F = 2 * (int)pv.layers * NC;
-    const TrainSeq seq{&pv, NC};
-    store_tile_g<kTR, kTW>(D.h, dh_store, kEmbed);
-    store_tile<kTR, kTW>(D.h, sm.xs);
+    const typename RowsTypes<BF>::Seq seq{&pv, NC};
+    if constexpr (BF) {
+        store_tile_g_b<kTR, kTW>(D.h, dh_store, kEmbed);
+        store_tile_relu_b<kTR, kTW, false>(D.h, sm.xb);
+    } else {
+        store_tile_g<kTR, kTW>(D.h, dh_store, kEmbed);
+        store_tile<kTR, kTW>(D.h, sm.xs);
+    }
     __syncthreads();
     TRegs G;
     zero<kTR, kTW>(G.h);
@@ -184,17 +228,29 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem
         for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
             mask[rt][ct][r] = v_tile[(size_t)row * H + kChunk * c + col];
         });
-        float* vs = sm.vs[c & 1];  // double-buffered: no barrier before the write
         TS::Acc v[TS::RT][TS::CT];
         zero<kTR, kTW>(v);
-        ws.template gemm<0>(v, sm.xs, s, seq);
-        for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-            const float g = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
-            dv_store[(size_t)row * H + kChunk * c + col] = g;
-            vs[row * kLds + col] = g;
-        });
-        __syncthreads();
-        ws.template gemm<1>(G.h, vs, s + 1, seq);
+        if constexpr (BF) {
+            uint16_t* vb = sm.vb[c & 1];  // double-buffered: no barrier before the write
+            ws.template gemm<0>(v, sm.xb, s, seq);
+            for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
+                const uint16_t g = bf16_rne(mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f);
+                dv_store[(size_t)row * H + kChunk * c + col] = bf16_to_float(g);
+                vb[row * kLdsB + col] = g;
+            });
+            __syncthreads();
+            ws.template gemm<1>(G.h, vb, s + 1, seq);
+        } else {
+            float* vs = sm.vs[c & 1];  // double-buffered: no barrier before the write
+            ws.template gemm<0>(v, sm.xs, s, seq);
+            for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
+                const float g = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
+                dv_store[(size_t)row * H + kChunk * c + col] = g;
+                vs[row * kLds + col] = g;
+            });
+            __syncthreads();
+            ws.template gemm<1>(G.h, vs, s + 1, seq);
+        }
     }
     __syncthreads();
     bwd_layernorm(sm, G, xn_tile, sd_tile, gamma, tp + pv.off_ln_gamma[l], tp + pv.off_ln_beta[l], scratch);
@@ -206,8 +262,9 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, TSmem
 
 // LDS of one train_rows workgroup, sized for every supported shape. The LN
 // captures xn / sd are only read by the LN backward, so they never leave the CU.
+template <bool BF>
 struct RowsSmem {
-    TSmem sm;
+    typename RowsTypes<BF>::Smem sm;
     float xn[(MG_MAX_LAYERS + 1) * kTR * kEmbed];
     float sd[(MG_MAX_LAYERS + 1) * kTR];
     float ln[(MG_MAX_LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
@@ -220,11 +277,13 @@ struct RowsSmem {
     float scratch[kTNT];
 };
 
+// BF: the block GEMMs take bf16 operands (MG_PRECISION_BF16).
+template <bool BF>
 __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     constexpr int M = kTR;
-    using Stream = TStream<kTR, kTW>;
-    __shared__ RowsSmem L;
-    TSmem& sm = L.sm;
+    using Stream = typename RowsTypes<BF>::Stream;
+    __shared__ RowsSmem<BF> L;
+    auto& sm = L.sm;
     TRegs R;
     const mg_policy_view& pv = a.pv;
     const TrainWs& ws = a.ws;
@@ -264,16 +323,21 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
         if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
     }
     Stream wst;
-    const TrainSeq seq{&pv, H / kChunk};
+    const typename RowsTypes<BF>::Seq seq{&pv, H / kChunk};
     wst.start(4 * NL * (H / kChunk), seq);
     __syncthreads();
 
     // ---- forward with capture ----
     fwd_embed<M, kTW>(winL, binL, L.obs, O, R);
     for (int l = 0; l < NL; ++l) {
+        uint16_t* xb = nullptr;
+        if constexpr (BF) xb = sm.xb;
         fwd_layernorm<M, kTW>(sm, R, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, L.xn + l * M * kEmbed,
-                              L.sd + l * M, ws.x + ((size_t)l * B + r0) * kEmbed);
-        fwd_block<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H, seq);
+                              L.sd + l * M, ws.x + ((size_t)l * B + r0) * kEmbed, xb);
+        if constexpr (BF)
+            fwd_block_b<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H, seq);
+        else
+            fwd_block<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H, seq);
     }
     // the backward's first weights are in flight through the final LN, the head and the loss
     fwd_layernorm<M, kTW>(sm, R, L.ln + NL * 2 * kEmbed, L.ln + NL * 2 * kEmbed + kEmbed, L.xn + NL * M * kEmbed,
@@ -381,7 +445,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     bwd_layernorm(sm, D, L.xn + NL * M * kEmbed, L.sd + NL * M, L.ln + NL * 2 * kEmbed, tp + pv.off_ln_gamma[NL],
                   tp + pv.off_ln_beta[NL], L.scratch);
     for (int l = NL - 1; l >= 0; --l) {
-        bwd_block(pv, l, sm, D, wst, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
+        bwd_block<BF>(pv, l, sm, D, wst, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
                   ws.dhb + ((size_t)l * B + r0) * kEmbed, L.xn + l * M * kEmbed, L.sd + l * M,
                   L.ln + l * 2 * kEmbed, tp, L.scratch);
     }
@@ -606,16 +670,28 @@ __device__ __forceinline__ u32x4 pack_bf16_column(const float* lds, int k0, int 
     return w;
 }
 
+// Packs lds[n * kTileLd + k0 + i], i = 0..7, as eight bf16 (16 bytes).
+__device__ __forceinline__ u32x4 pack_bf16_row(const float* lds, int n, int k0) {
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)bf16_rne(lds[n * kTileLd + k0 + 2 * j]) |
+               ((uint32_t)bf16_rne(lds[n * kTileLd + k0 + 2 * j + 1]) << 16);
+    return w;
+}
+
 // Writes the tile held in lds ([r][c], stride kTileLd) to the fragment-tiled
 // copies: frag_fwd32 and frag_fwd16 read its transpose (rows n = c,
 // contraction k = r, K = rows), frag_bwd16 the matrix as stored (n = r, k = c,
 // K = cols). Each thread writes one float4 (four consecutive k of one n) to
-// each; a wave's 64 float4s form one 1 KB run. The bf16 copies of the
-// transpose (when given) take 8 k per thread: threads 0-127 the 32-wide strip
-// (two k-groups of 16), threads 128-255 the two 16-wide strips (one k-group of
-// 32). Starts with a barrier.
+// each; a wave's 64 float4s form one 1 KB run. The bf16 copies (when given)
+// take 8 k per thread: threads 0-127 the transpose's 32-wide strip (two
+// k-groups of 16) and the matrix's two 16-wide strips, threads 128-255 the
+// transpose's two 16-wide strips (one k-group of 32 each). Starts with a
+// barrier.
 __device__ __forceinline__ void store_tile_frags(const MatTile& m, const float* lds, float* fwd32, float* fwd16,
-                                                 float* bwd16, uint16_t* fwd32b, uint16_t* fwd16b) {
+                                                 float* bwd16, uint16_t* fwd32b, uint16_t* fwd16b,
+                                                 uint16_t* bwd16b) {
     __syncthreads();
     const int t = threadIdx.x;
     {  // 32-wide strips: the tile is one strip's four k-groups, 4 KB in a row
@@ -639,6 +715,9 @@ __device__ __forceinline__ void store_tile_frags(const MatTile& m, const float* 
             const int ln = t & 63, nb = ln & 31, kb = 16 * (t >> 6) + 8 * (ln >> 5);
             *reinterpret_cast<u32x4*>(fwd32b + m.base + frag_index_b<32>(m.c0 + nb, m.r0 + kb, m.rows)) =
                 pack_bf16_column(lds, kb, nb);
+            const int nr = 16 * (t >> 6) + (ln & 15), kr = 8 * (ln >> 4);
+            *reinterpret_cast<u32x4*>(bwd16b + m.base + frag_index_b<16>(m.r0 + nr, m.c0 + kr, m.cols)) =
+                pack_bf16_row(lds, nr, kr);
         } else {
             const int t2 = t - 128, ln = t2 & 63, nb = 16 * (t2 >> 6) + (ln & 15), kb = 8 * (ln >> 4);
             *reinterpret_cast<u32x4*>(fwd16b + m.base + frag_index_b<16>(m.c0 + nb, m.r0 + kb, m.rows)) =
@@ -650,8 +729,8 @@ __device__ __forceinline__ void store_tile_frags(const MatTile& m, const float* 
 // The fragment-tiled copies from params, one tile per workgroup.
 __global__ void __launch_bounds__(256) derive_blocks_kernel(const float* __restrict__ param, float* __restrict__ fwd32,
                                                             float* __restrict__ fwd16, float* __restrict__ bwd16,
-                                                            uint16_t* fwd32b, uint16_t* fwd16b, uint32_t float_group,
-                                                            uint32_t H) {
+                                                            uint16_t* fwd32b, uint16_t* fwd16b, uint16_t* bwd16b,
+                                                            uint32_t float_group, uint32_t H) {
     __shared__ float lds[kTT * kTileLd];
     const MatTile m = mat_tile(blockIdx.x, float_group, H);
     const int t = threadIdx.x, c = t & (kTT - 1);
@@ -660,7 +739,7 @@ __global__ void __launch_bounds__(256) derive_blocks_kernel(const float* __restr
         const int r = (256 / kTT) * e + t / kTT;
         lds[r * kTileLd + c] = param[m.base + (size_t)(m.r0 + r) * m.cols + m.c0 + c];
     }
-    store_tile_frags(m, lds, fwd32, fwd16, bwd16, fwd32b, fwd16b);
+    store_tile_frags(m, lds, fwd32, fwd16, bwd16, fwd32b, fwd16b, bwd16b);
 }
 
 struct AdamArgs {
@@ -670,6 +749,7 @@ struct AdamArgs {
     float* frag_bwd16;
     uint16_t* frag_fwd32_bf;
     uint16_t* frag_fwd16_bf;
+    uint16_t* frag_bwd16_bf;
     const float* grad;
     float* mom;
     float* var;
@@ -740,7 +820,8 @@ __global__ void __launch_bounds__(256) adam_kernel(const AdamArgs a) {
             const int r = (256 / kTT) * e + t / kTT;
             lds[r * kTileLd + c] = adam_elem(a, idx[e], in[e], scale);
         }
-        store_tile_frags(m, lds, a.frag_fwd32, a.frag_fwd16, a.frag_bwd16, a.frag_fwd32_bf, a.frag_fwd16_bf);
+        store_tile_frags(m, lds, a.frag_fwd32, a.frag_fwd16, a.frag_bwd16, a.frag_fwd32_bf, a.frag_fwd16_bf,
+                         a.frag_bwd16_bf);
         return;
     }
     const uint32_t j = (blockIdx.x - a.mat_tiles) * 256 + t;
@@ -823,7 +904,8 @@ int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv) {
     int rc = check_matrix_layout(pv);
     if (rc) return rc;
     hipLaunchKernelGGL(dev::derive_blocks_kernel, dim3(mat_tiles(pv)), dim3(256), 0, st, pv.params, pv.frag_fwd32,
-                       pv.frag_fwd16, pv.frag_bwd16, pv.frag_fwd32_bf, pv.frag_fwd16_bf, pv.float_group, pv.hidden);
+                       pv.frag_fwd16, pv.frag_bwd16, pv.frag_fwd32_bf, pv.frag_fwd16_bf, pv.frag_bwd16_bf,
+                       pv.float_group, pv.hidden);
     MG_HIP(hipGetLastError(), "derive blocks launch");
     return MG_OK;
 }
@@ -856,7 +938,10 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         ra.logp_slots = logp_slots;
         ra.adv_stats = adv_stats;
         ra.head_out = head_out;
-        hipLaunchKernelGGL(dev::train_rows_kernel, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
+        if (pv.precision == MG_PRECISION_BF16)
+            hipLaunchKernelGGL(dev::train_rows_kernel<true>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
+        else
+            hipLaunchKernelGGL(dev::train_rows_kernel<false>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         MG_HIP(hipGetLastError(), "train rows launch");
     }
     {  // 2. block-matrix weight gradients
@@ -914,6 +999,7 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         aa.frag_bwd16 = pv.frag_bwd16;
         aa.frag_fwd32_bf = pv.frag_fwd32_bf;
         aa.frag_fwd16_bf = pv.frag_fwd16_bf;
+        aa.frag_bwd16_bf = pv.frag_bwd16_bf;
         aa.grad = ws.grad;
         aa.mom = m;
         aa.var = v;

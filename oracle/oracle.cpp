@@ -484,12 +484,13 @@ void forward_row(const Net& n, const float* obs, float* head, float* xn_out, flo
     for (uint32_t l = 0; l < n.NL; ++l) {
         float sd;
         ln_forward(h.data(), n.P + n.L.off_ln_gamma[l], n.P + n.L.off_ln_beta[l], E, xn.data(), x.data(), &sd);
+        const bool bf = n.d.bf16 != 0;
         if (xn_out) std::memcpy(xn_out + l * E, xn.data(), E * 4);
-        if (x_out) std::memcpy(x_out + l * E, x.data(), E * 4);
+        if (x_out)  // the up GEMM's operand (rounded in bf16 mode), for dUp
+            for (uint32_t k = 0; k < E; ++k) x_out[l * E + k] = bf ? round_bf16(x[k]) : x[k];
         if (sd_out) sd_out[l] = sd;
         // model/mlp.metal:18-58: V = X Up, relu (bf16 operands: X and Up rounded)
         const float* Up = n.P + n.L.off_up[l];
-        const bool bf = n.d.bf16 != 0;
         std::fill(v.begin(), v.end(), 0.0f);
         for (uint32_t k = 0; k < E; ++k) {
             float xk = bf ? round_bf16(x[k]) : x[k];
@@ -500,7 +501,8 @@ void forward_row(const Net& n, const float* obs, float* head, float* xn_out, flo
                 for (uint32_t j = 0; j < H; ++j) v[j] += xk * row[j];
         }
         for (uint32_t j = 0; j < H; ++j) v[j] = v[j] > 0.0f ? v[j] : 0.0f;
-        if (v_out) std::memcpy(v_out + (size_t)l * H, v.data(), H * 4);
+        if (v_out)  // the down GEMM's operand (rounded in bf16 mode), for dDown and the relu mask
+            for (uint32_t j = 0; j < H; ++j) v_out[(size_t)l * H + j] = bf ? round_bf16(v[j]) : v[j];
         // model/mlp.metal:60-86: Out = V Down (bf16 operands: V and Down rounded);
         // model/elementwise.metal:4-13 residual add
         const float* Dn = n.P + n.L.off_down[l];
@@ -933,21 +935,26 @@ void orc_train_minibatch(const orc_dims* dp, const orc_hparams* hp, float* P, fl
             ln_backward(dx.data(), &xn[r * actW + NL * E], P + L.off_ln_gamma[NL], sd[(size_t)r * (NL + 1) + NL], E,
                         dh.data());
             for (int l = (int)NL - 1; l >= 0; --l) {
-                std::memcpy(&dhb[((size_t)r * NL + l) * E], dh.data(), E * 4);
+                // bf16 mode: dh and dV enter their GEMMs (and the weight
+                // gradients) rounded, and so do the weights
+                const bool bf = d.bf16 != 0;
+                auto q = [bf](float z) { return bf ? round_bf16(z) : z; };
+                for (uint32_t c = 0; c < E; ++c) dhb[((size_t)r * NL + l) * E + c] = q(dh[c]);
+                const float* dhq = &dhb[((size_t)r * NL + l) * E];
                 const float* Dn = P + L.off_down[l];
                 const float* Up = P + L.off_up[l];
                 const float* vrow = &vv[((size_t)r * NL + l) * H];
                 for (uint32_t j = 0; j < H; ++j) {  // model/mlp.metal:88-127
                     float acc = 0.0f;
                     const float* row = Dn + (size_t)j * E;
-                    for (uint32_t c = 0; c < E; ++c) acc += dh[c] * row[c];
-                    dv[j] = vrow[j] > 0.0f ? acc : 0.0f;
+                    for (uint32_t c = 0; c < E; ++c) acc += dhq[c] * q(row[c]);
+                    dv[j] = q(vrow[j] > 0.0f ? acc : 0.0f);
                 }
                 std::memcpy(&dvb[((size_t)r * NL + l) * H], dv.data(), H * 4);
                 for (uint32_t k = 0; k < E; ++k) {  // model/mlp.metal:131-153
                     float acc = 0.0f;
                     const float* row = Up + (size_t)k * H;
-                    for (uint32_t j = 0; j < H; ++j) acc += dv[j] * row[j];
+                    for (uint32_t j = 0; j < H; ++j) acc += dv[j] * q(row[j]);
                     dx[k] = acc;
                 }
                 std::memcpy(&dxl[r * actW + (size_t)l * E], dx.data(), E * 4);

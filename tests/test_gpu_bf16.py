@@ -39,3 +39,54 @@ def test_bf16_forward_matches_oracle_and_differs_from_fp32(mg, orc, env):
     gap = float((np.abs(head - fp32) / np.maximum(1.0, np.abs(fp32))).max())
     print(f"bf16 head vs bf16 oracle {err:.2e}, vs fp32 oracle {gap:.2e}")
     assert gap > 3 * err, (gap, err)
+
+
+@pytest.mark.parametrize("env,n,B,block", [("cartpole", 2048, 512, 3), ("cartpole_continuous", 2048, 1024, 1),
+                                           ("voxelnav16", 1024, 512, 2)])
+def test_bf16_minibatch(mg, orc, env, n, B, block):
+    """One PPO minibatch in bf16 mode against the oracle's bf16 train step on
+    the GPU's own rollout: recomputed head (median/p99/max), the Adam first
+    moment (0.1 x the clipped gradient) per parameter group, post-Adam weights
+    and LossStats."""
+    from parity import TOL_TRAIN, assert_close
+    from test_gpu_train import block_rows, group_errors
+
+    eid, kernel = ENVS[env]
+    T = 2
+    gym = mg.Gym(kernel, n, 0)
+    model = mg.PPOModel(gym, horizon=T, minibatch=B, precision="bf16")
+    d = orc.dims(eid, bf16=True)
+    model.collect()
+    s = model.download_slots()
+    p0 = model.params()
+    model.train_block(block)
+    hp = orc.hparams()
+    P, M, V = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    st, grad, head = orc.train_minibatch(d, hp, P, M, V, 1, *block_rows(s, n, B, block), threads=THREADS)
+    assert_close_bf16(model.head(), head, "recomputed head")
+    m1, _, _ = model.adam_state()
+    errs = group_errors(model.pv, m1, M)
+    print("bf16 moment, gpu vs oracle per group:", errs)
+    assert max(errs.values()) < 1e-2, errs
+    # the same gradient computed in fp32 is much further away
+    P2, M2, V2 = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    orc.train_minibatch(orc.dims(eid), hp, P2, M2, V2, 1, *block_rows(s, n, B, block), threads=THREADS)
+    e32 = group_errors(model.pv, M2, M)
+    assert e32["up0"] > 3 * errs["up0"], (e32["up0"], errs["up0"])
+    assert_close(model.params(), P, TOL_TRAIN, "post-Adam weights")
+    got, want = np.array(model.last_stats().as_tuple()), np.array(st.as_tuple())
+    assert_close(got[[0, 1, 2, 3, 5]], want[[0, 1, 2, 3, 5]], TOL_TRAIN, "LossStats")
+
+
+def test_bf16_full_loop_learns(mg):
+    """CartPole trained in bf16 mode improves its mean episode length."""
+    gym = mg.Gym("rollout_cartpole", 4096, 0)
+    model = mg.PPOModel(gym, horizon=32, precision="bf16")
+    lens = []
+    for it in range(12):
+        model.collect()
+        d = model.download_slots()["done"]
+        lens.append(d.size / max(1, d.sum()))
+        model.train(4)
+        assert np.all(np.isfinite(model.last_stats().as_tuple()))
+    assert np.mean(lens[-3:]) > 1.5 * np.mean(lens[:3]), lens
