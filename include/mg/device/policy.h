@@ -319,8 +319,7 @@ __device__ __forceinline__ void fwd_embed(const float* Win, const float* bias, c
 // If xn_out/sd_out/x_out are given, the normalised values, the standard
 // deviation and the output are also written there ([M][128], [M], [M][128],
 // row-major; global memory or LDS) for the backward pass; if xb_out is given,
-// the output rounded to bfloat16 goes there too ([M] rows of stride kLdsB) and
-// x_out receives the rounded values (the operand the bf16 GEMMs see).
+// the output rounded to bfloat16 goes there too ([M] rows of stride kLdsB).
 // Smem is any shared-memory layout with an fp32 xs tile.
 constexpr int kLdsB = kEmbed + 8;  // LDS row stride of a bfloat16 tile (elements)
 template <int M, int W = 4, class Smem>
@@ -373,13 +372,8 @@ __device__ __forceinline__ void fwd_layernorm(Smem& sm, const FwdRegs<M, W>& R, 
             const uint32_t lo = (uint32_t)hb[0] | ((uint32_t)hb[1] << 16);
             const uint32_t hi = (uint32_t)hb[2] | ((uint32_t)hb[3] << 16);
             *reinterpret_cast<uint2*>(xb_out + row * kLdsB + c0 + c) = make_uint2(lo, hi);
-            if (x_out) {
-                f32x4 ob;
-#pragma unroll
-                for (int u = 0; u < 4; ++u) ob[u] = bf16_to_float(hb[u]);
-                *reinterpret_cast<f32x4*>(x_out + row * kEmbed + c0 + c) = ob;
-            }
-        } else if (x_out) {
+        }
+        if (x_out) {
             *reinterpret_cast<f32x4*>(x_out + row * kEmbed + c0 + c) = o;
         }
     }

@@ -206,24 +206,32 @@ __device__ __forceinline__ void store_tile_relu_b(const AccTile<M, W>& acc, uint
     });
 }
 
-// Writes a register tile rounded to bfloat16 (kept as floats) to global
-// memory (global[row * ld + col]), optionally through relu: the captured
-// operand of a bf16 GEMM.
-template <int M, int W = 4, bool RELU = false>
-__device__ __forceinline__ void store_tile_g_b(const AccTile<M, W>& acc, float* global, size_t ld) {
-    for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
-        float x = acc[rt][ct][r];
-        if (RELU) x = x > 0.0f ? x : 0.0f;
-        global[(size_t)row * ld + col] = bf16_to_float(bf16_rne(x));
-    });
+// Row-group-packed layout of a bf16 matrix with C columns (the operand
+// layout of the weight-gradient GEMMs, which contract over rows): element
+// (r, c) at ((r / 8) C + c) 8 + r % 8, so 8 consecutive rows of one column are
+// 16 contiguous bytes. Copies rows 0 .. 15 of a bf16 LDS tile (row stride
+// kLdsB, 128 columns) to columns col0 .. col0 + 127 of such a matrix; g points
+// at the tile's first row group (a multiple of 16 rows). NT threads.
+template <int NT>
+__device__ __forceinline__ void copy_tile_p8(const uint16_t* lds, uint16_t* g, uint32_t C, uint32_t col0) {
+    for (int i = threadIdx.x; i < 2 * kEmbed; i += NT) {
+        const int grp = i / kEmbed, c = i % kEmbed;
+        const uint16_t* col = lds + 8 * grp * kLdsB + c;
+        u32x4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = (uint32_t)col[2 * j * kLdsB] | ((uint32_t)col[(2 * j + 1) * kLdsB] << 16);
+        *reinterpret_cast<u32x4*>(g + ((size_t)grp * C + col0 + c) * 8) = w;
+    }
 }
 
 // One residual block with bf16 GEMM operands: h += relu(xb Up) Down, chunked
 // as in fwd_block; sm.xb holds the block input's LN output in bf16. With VOUT
-// the rounded relu'd hidden activations are also written to v_out.
+// (16-row tiles) the relu'd hidden chunks, as the down GEMM saw them, are also
+// written to v_out (row-group-packed, H columns, at the tile's first row group).
 template <int M, int W, bool VOUT, int NV, class Seq, class Stream>
 __device__ __forceinline__ void fwd_block_b(const mg_policy_view& pv, int l, FwdSmemB<M, NV>& sm,
-                                            FwdRegs<M, W>& R, Stream& ws, float* v_out, Seq seq) {
+                                            FwdRegs<M, W>& R, Stream& ws, uint16_t* v_out, Seq seq) {
     using S = Shape<M, W>;
     const int H = (int)pv.hidden, NC = H / kChunk;
     for (int c = 0; c < NC; ++c) {
@@ -232,10 +240,13 @@ __device__ __forceinline__ void fwd_block_b(const mg_policy_view& pv, int l, Fwd
         typename S::Acc v[S::RT][S::CT];
         zero<M, W>(v);
         ws.template gemm<0>(v, sm.xb, s, seq);
-        if constexpr (VOUT) store_tile_g_b<M, W, true>(v, v_out + kChunk * c, H);
         if constexpr (NV == 1) __syncthreads();  // every wave is done reading the previous chunk from vb
         store_tile_relu_b<M, W>(v, vb);
         __syncthreads();
+        if constexpr (VOUT) {
+            static_assert(M == 16, "captures are 16-row tiles");
+            copy_tile_p8<S::NT>(vb, v_out, H, kChunk * c);
+        }
         ws.template gemm<1>(R.h, vb, s + 1, seq);
     }
 }

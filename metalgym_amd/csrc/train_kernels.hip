@@ -7,8 +7,9 @@
 //     activations and gradients the weight gradients need.
 //     The same workgroup writes its tile's sums of the vector-parameter, head
 //     and log_std gradients and of the loss statistics.
-//  2. train_dw: the block matrices' gradients X^T dY as LDS-staged 64x64
-//     MFMA tiles, the rows split into ranges.
+//  2. train_dw: the block matrices' gradients X^T dY as 64x64 MFMA tiles,
+//     the rows split into ranges (fp32: LDS-staged slabs; bf16: operands
+//     loaded straight into registers from row-group-packed captures).
 //  3. grad_reduce: sums the tile partials and the row splits in fixed order,
 //     writes the minibatch's LossStats (model/ppo.h:925-943) and one partial
 //     squared norm per workgroup.
@@ -183,17 +184,21 @@ struct TrainSeqB {
 };
 
 // The row pass's types per precision: LDS tile, weight stream, GEMM sequence.
+// The captures for the weight gradients (Cap): fp32 row-major, or bf16
+// row-group-packed (copy_tile_p8) as the bf16 weight-gradient GEMMs read them.
 template <bool BF>
 struct RowsTypes {
     using Smem = TSmem;
     using Stream = TStream<kTR, kTW>;
     using Seq = TrainSeq;
+    using Cap = float;
 };
 template <>
 struct RowsTypes<true> {
     using Smem = TSmemB;
     using Stream = TStreamB<kTR, kTW>;
     using Seq = TrainSeqB;
+    using Cap = uint16_t;
 };
 
 // Backward of block l (model/mlp.metal:88-153 + model/ppo.h:851-852). D holds
@@ -202,22 +207,23 @@ struct RowsTypes<true> {
 // masked by relu, then dx += dV_c Up_c^T; ws streams the row pass's TrainSeq.
 // With BF the two GEMMs take bf16 operands (dh and dV rounded as they are
 // written to LDS; the captures for the weight gradients are the rounded
-// values).
-template <bool BF, class Stream, class Smem>
+// values). v_tile, dv_store and dh_store point at the tile's first row.
+template <bool BF, class Stream, class Smem, class Cap = typename RowsTypes<BF>::Cap>
 __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, Smem& sm, TRegs& D,
-                                          Stream& ws, const float* v_tile, float* dv_store, float* dh_store,
+                                          Stream& ws, const Cap* v_tile, Cap* dv_store, Cap* dh_store,
                                           const float* xn_tile, const float* sd_tile, const float* gamma,
                                           float* tp, float* scratch) {
     const int H = (int)pv.hidden, NC = H / kChunk, F = 2 * (int)pv.layers * NC;
     const typename RowsTypes<BF>::Seq seq{&pv, NC};
     if constexpr (BF) {
-        store_tile_g_b<kTR, kTW>(D.h, dh_store, kEmbed);
         store_tile_relu_b<kTR, kTW, false>(D.h, sm.xb);
+        __syncthreads();
+        copy_tile_p8<kTNT>(sm.xb, dh_store, kEmbed, 0);
     } else {
         store_tile_g<kTR, kTW>(D.h, dh_store, kEmbed);
         store_tile<kTR, kTW>(D.h, sm.xs);
+        __syncthreads();
     }
-    __syncthreads();
     TRegs G;
     zero<kTR, kTW>(G.h);
     for (int c = 0; c < NC; ++c) {
@@ -226,7 +232,10 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, Smem&
         // refills (vector memory counters complete in order)
         TS::Acc mask[TS::RT][TS::CT];
         for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-            mask[rt][ct][r] = v_tile[(size_t)row * H + kChunk * c + col];
+            if constexpr (BF)  // row-group-packed
+                mask[rt][ct][r] = bf16_to_float(v_tile[((size_t)(row >> 3) * H + kChunk * c + col) * 8 + (row & 7)]);
+            else
+                mask[rt][ct][r] = v_tile[(size_t)row * H + kChunk * c + col];
         });
         TS::Acc v[TS::RT][TS::CT];
         zero<kTR, kTW>(v);
@@ -234,11 +243,10 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, Smem&
             uint16_t* vb = sm.vb[c & 1];  // double-buffered: no barrier before the write
             ws.template gemm<0>(v, sm.xb, s, seq);
             for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-                const uint16_t g = bf16_rne(mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f);
-                dv_store[(size_t)row * H + kChunk * c + col] = bf16_to_float(g);
-                vb[row * kLdsB + col] = g;
+                vb[row * kLdsB + col] = bf16_rne(mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f);
             });
             __syncthreads();
+            copy_tile_p8<kTNT>(vb, dv_store, H, kChunk * c);
             ws.template gemm<1>(G.h, vb, s + 1, seq);
         } else {
             float* vs = sm.vs[c & 1];  // double-buffered: no barrier before the write
@@ -329,19 +337,28 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
 
     // ---- forward with capture ----
     fwd_embed<M, kTW>(winL, binL, L.obs, O, R);
+    // the captures of layer l for rows r0 .. r0 + 15: [B][C] per layer; in the
+    // bf16 layout these rows start at row group r0 / 8, element r0 C, too
+    using Cap = typename RowsTypes<BF>::Cap;
+    Cap* const cx = reinterpret_cast<Cap*>(ws.x);
+    Cap* const cv = reinterpret_cast<Cap*>(ws.v);
+    Cap* const cdh = reinterpret_cast<Cap*>(ws.dhb);
+    Cap* const cdv = reinterpret_cast<Cap*>(ws.dvb);
     for (int l = 0; l < NL; ++l) {
-        uint16_t* xb = nullptr;
-        if constexpr (BF) xb = sm.xb;
-        fwd_layernorm<M, kTW>(sm, R, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, L.xn + l * M * kEmbed,
-                              L.sd + l * M, ws.x + ((size_t)l * B + r0) * kEmbed, xb);
-        if constexpr (BF)
-            fwd_block_b<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H, seq);
-        else
-            fwd_block<M, kTW, true, 2>(pv, l, sm, R, wst, ws.v + ((size_t)l * B + r0) * H, seq);
+        const float* gamma = L.ln + l * 2 * kEmbed;
+        if constexpr (BF) {
+            fwd_layernorm<M, kTW>(sm, R, gamma, gamma + kEmbed, L.xn + l * M * kEmbed, L.sd + l * M, nullptr, sm.xb);
+            copy_tile_p8<kTNT>(sm.xb, cx + ((size_t)l * B + r0) * kEmbed, kEmbed, 0);
+            fwd_block_b<M, kTW, true, 2>(pv, l, sm, R, wst, cv + ((size_t)l * B + r0) * H, seq);
+        } else {
+            fwd_layernorm<M, kTW>(sm, R, gamma, gamma + kEmbed, L.xn + l * M * kEmbed, L.sd + l * M,
+                                  cx + ((size_t)l * B + r0) * kEmbed);
+            fwd_block<M, kTW, true, 2>(pv, l, sm, R, wst, cv + ((size_t)l * B + r0) * H, seq);
+        }
     }
     // the backward's first weights are in flight through the final LN, the head and the loss
     fwd_layernorm<M, kTW>(sm, R, L.ln + NL * 2 * kEmbed, L.ln + NL * 2 * kEmbed + kEmbed, L.xn + NL * M * kEmbed,
-                          L.sd + NL * M, ws.x + ((size_t)NL * B + r0) * kEmbed);
+                          L.sd + NL * M);
     fwd_head<M, kTW>(L.wh, sm, L.head, HD);
 
     // ---- loss and head gradient: 32 threads per row, thread k owning head
@@ -445,9 +462,9 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     bwd_layernorm(sm, D, L.xn + NL * M * kEmbed, L.sd + NL * M, L.ln + NL * 2 * kEmbed, tp + pv.off_ln_gamma[NL],
                   tp + pv.off_ln_beta[NL], L.scratch);
     for (int l = NL - 1; l >= 0; --l) {
-        bwd_block<BF>(pv, l, sm, D, wst, ws.v + ((size_t)l * B + r0) * H, ws.dvb + ((size_t)l * B + r0) * H,
-                  ws.dhb + ((size_t)l * B + r0) * kEmbed, L.xn + l * M * kEmbed, L.sd + l * M,
-                  L.ln + l * 2 * kEmbed, tp, L.scratch);
+        bwd_block<BF>(pv, l, sm, D, wst, cv + ((size_t)l * B + r0) * H, cdv + ((size_t)l * B + r0) * H,
+                      cdh + ((size_t)l * B + r0) * kEmbed, L.xn + l * M * kEmbed, L.sd + l * M,
+                      L.ln + l * 2 * kEmbed, tp, L.scratch);
     }
     // model/input.metal:38-60 on this tile: dW_in[k][c] = sum_r obs[r][k] dh0[r][c], db_in = sum_r dh0
     store_tile<M, kTW>(D.h, sm.xs);
@@ -458,19 +475,23 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
 
 // ---- weight gradients ---------------------------------------------------------
 
-// A big tile job: C[m][n] = sum_r X[r][m] Y[r][n] for a 128 x H (or H x 128) matrix.
-struct BigMat {
-    const float* x;
-    const float* y;
-    uint32_t ldx, ldy;  // row strides
+// A big tile job: C[m][n] = sum_r X[r][m] Y[r][n] for a 128 x H (or H x 128)
+// matrix; X and Y are the captures (T = float: row-major; T = uint16_t: bf16,
+// row-group-packed), ldx / ldy their column counts.
+template <class T>
+struct BigMatT {
+    const T* x;
+    const T* y;
+    uint32_t ldx, ldy;
     uint32_t mdim, ndim;
     uint32_t off;
     uint32_t pad;
 };
 constexpr int kMaxBig = 2 * MG_MAX_LAYERS;
 
-struct DwArgs {
-    BigMat big[kMaxBig];
+template <class T>
+struct DwArgsT {
+    BigMatT<T> big[kMaxBig];
     uint32_t nbig;
     uint32_t tiles_per_big[kMaxBig];
     uint32_t big_tiles;    // total 64x64 tiles over all big matrices
@@ -487,7 +508,7 @@ constexpr int kDwLd = 64 + 4;  // LDS row stride of a staged 64-wide slab
 // robin, so with 8 or 16 splits all tiles of one row split run on the same XCD
 // and read its rows through that XCD's L2 (each row is fetched from memory
 // about once instead of once per tile sharing it).
-__global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
+__global__ void __launch_bounds__(256) train_dw_kernel(const DwArgsT<float> a) {
     __shared__ float xs[2][kDwRows * kDwLd];
     __shared__ float ys[2][kDwRows * kDwLd];
     const uint32_t split = blockIdx.x % a.splits, tile = blockIdx.x / a.splits;
@@ -498,7 +519,7 @@ __global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
     if (tile < a.big_tiles) {
         uint32_t t = tile, m = 0;
         while (t >= a.tiles_per_big[m]) t -= a.tiles_per_big[m], ++m;
-        const BigMat& bm = a.big[m];
+        const BigMatT<float>& bm = a.big[m];
         const uint32_t ntn = bm.ndim / 64;
         const uint32_t tm = t / ntn, tn = t % ntn;
         const int w = tid >> 6, lane = tid & 63, nn = lane & 31, hh = lane >> 5;
@@ -555,6 +576,94 @@ __global__ void __launch_bounds__(256) train_dw_kernel(const DwArgs a) {
             out[bm.off + (size_t)row * bm.ndim + tn * 64 + wn + nn] = acc[r];
         }
         return;
+    }
+}
+
+// The weight gradients with bf16 operands (MG_PRECISION_BF16). X and Y are
+// row-group-packed (element (r, c) at ((r / 8) C + c) 8 + r % 8), so the
+// operand of lane l of a v_mfma_f32_32x32x16_bf16 contracting over rows (rows
+// 8 (l / 32) .. + 7 of column l % 32) is 16 contiguous bytes, and a half-wave
+// reads 512 contiguous bytes: operands go from memory straight into
+// registers, no LDS staging. A workgroup computes one 64 x 64 tile over its
+// row split (workgroup id = tile * splits + split, as in train_dw_kernel);
+// each of its NW waves takes every NW-th 16-row step, with the whole tile as
+// 2 x 2 MFMAs per step, and the NW partial tiles are added in LDS in wave
+// order. U steps are loaded while the previous U run their MFMAs. (Measured at
+// 4096 rows, 2 blocks, hidden 512: 4 or 8 waves, U = 2 or 4 and 4 or 8 row
+// splits all ran within 3% of each other, about 10 us.)
+constexpr int kDwbWaves = 4;
+template <int NW, int U>
+__global__ void __launch_bounds__(64 * NW) train_dw_bf16_kernel(const DwArgsT<uint16_t> a) {
+    __shared__ float red[NW][64 * 64];
+    const uint32_t split = blockIdx.x % a.splits, tile = blockIdx.x / a.splits;
+    const uint32_t rowsPer = a.rows / a.splits;  // a multiple of 16 NW
+    const uint32_t rb = split * rowsPer;
+    uint32_t t = tile, m = 0;
+    while (t >= a.tiles_per_big[m]) t -= a.tiles_per_big[m], ++m;
+    const BigMatT<uint16_t>& bm = a.big[m];
+    const uint32_t ntn = bm.ndim / 64;
+    const uint32_t tm = t / ntn, tn = t % ntn;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // lane's operands in step s: row group rb / 8 + 2 (NW s + w) + lane / 32,
+    // columns tile + lane % 32 and tile + 32 + lane % 32
+    const size_t g0 = rb / 8 + 2 * w + (lane >> 5);
+    const uint16_t* xp = bm.x + (g0 * bm.ldx + tm * 64 + (lane & 31)) * 8;
+    const uint16_t* yp = bm.y + (g0 * bm.ldy + tn * 64 + (lane & 31)) * 8;
+    const size_t xstep = (size_t)16 * NW * bm.ldx, ystep = (size_t)16 * NW * bm.ldy;  // 2 NW row groups
+    const uint32_t steps = rowsPer / (16 * NW);
+    const uint32_t batches = (steps + U - 1) / U;
+    // steps past the split's end load zeros (they add nothing)
+    auto load = [&](u32x4 (&op)[U][4], uint32_t b) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t st = b * U + u;
+            if (st < steps) {
+                const uint16_t* x = xp + st * xstep;
+                const uint16_t* y = yp + st * ystep;
+                op[u][0] = *reinterpret_cast<const u32x4*>(x);
+                op[u][1] = *reinterpret_cast<const u32x4*>(x + 256);
+                op[u][2] = *reinterpret_cast<const u32x4*>(y);
+                op[u][3] = *reinterpret_cast<const u32x4*>(y + 256);
+            } else {
+                op[u][0] = op[u][1] = op[u][2] = op[u][3] = u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    u32x4 cur[U][4], nxt[U][4];
+    load(cur, 0);
+    for (uint32_t b = 0; b < batches; ++b) {
+        if (b + 1 < batches) load(nxt, b + 1);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = ShapeB<32>::mfma(cur[u][i], cur[u][2 + j], acc[i][j]);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cur[u][k] = nxt[u][k];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                red[w][(32 * i + c32_row(r, lane)) * 64 + 32 * j + (lane & 31)] = acc[i][j][r];
+    __syncthreads();
+    float* out = a.partial + (size_t)split * a.count + bm.off + (size_t)tm * 64 * bm.ndim + tn * 64;
+    for (int e = threadIdx.x; e < 64 * 64; e += 64 * NW) {
+        float v = red[0][e];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) v += red[q][e];
+        out[(size_t)(e >> 6) * bm.ndim + (e & 63)] = v;
     }
 }
 
@@ -851,7 +960,7 @@ WsPlan plan(const mg_policy_view& pv, uint32_t B) {
     WsPlan p;
     p.tp_count = (uint32_t)align256(pv.float_group + E * HD + 5);
     const size_t sizes[8] = {
-        (L + 1) * B * E * 4,                       // x
+        L * B * E * 4,                             // x
         L * B * H * 4,                             // v
         L * B * E * 4,                             // dhb
         L * B * H * 4,                             // dvb
@@ -910,6 +1019,37 @@ int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv) {
     return MG_OK;
 }
 
+// The weight-gradient jobs of one minibatch: per block, dUp and dDown from
+// the captures (T: their element type); 64 x 64 tiles.
+template <class T>
+dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B, uint32_t splits) {
+    const uint32_t E = MG_EMBED, H = pv.hidden;
+    const T* x = reinterpret_cast<const T*>(ws.x);
+    const T* v = reinterpret_cast<const T*>(ws.v);
+    const T* dh = reinterpret_cast<const T*>(ws.dhb);
+    const T* dv = reinterpret_cast<const T*>(ws.dvb);
+    dev::DwArgsT<T> da;
+    memset(&da, 0, sizeof(da));
+    da.rows = B;
+    da.splits = splits;
+    da.count = pv.count;
+    da.partial = ws.partial;
+    uint32_t nb = 0, tiles = 0;
+    for (uint32_t l = 0; l < pv.layers; ++l) {
+        // dUp_l[k][j] = sum_r x_l[r][k] dV_l[r][j]  (model/mlp.metal:201-203)
+        da.big[nb] = {x + (size_t)l * B * E, dv + (size_t)l * B * H, E, H, E, H, pv.off_up[l], 0};
+        da.tiles_per_big[nb] = (E / 64) * (H / 64);
+        tiles += da.tiles_per_big[nb++];
+        // dDown_l[j][c] = sum_r V_l[r][j] dh_l[r][c]  (model/mlp.metal:205-207)
+        da.big[nb] = {v + (size_t)l * B * H, dh + (size_t)l * B * E, H, E, H, E, pv.off_down[l], 0};
+        da.tiles_per_big[nb] = (H / 64) * (E / 64);
+        tiles += da.tiles_per_big[nb++];
+    }
+    da.nbig = nb;
+    da.big_tiles = tiles;
+    return da;
+}
+
 int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hparams& hp, float lr,
                       const TrainWs& ws, const TrainStep& step, const float* obs_slots, const void* action_slots,
                       const float* adv_slots, const float* ret_slots, const float* logp_slots,
@@ -918,11 +1058,18 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
     MG_CHECK(B % 64 == 0, MG_ERR_INVALID, "train: minibatch %u must be a multiple of 64", B);
     MG_CHECK(pv.obs_dim <= (uint32_t)dev::kMaxObsT && pv.head_dim <= (uint32_t)dev::kMaxHeadT, MG_ERR_INVALID,
              "train: OBS_DIM <= 64 and ACT_DIM + 1 <= 64 required");
-    // row splits of the block-matrix gradient sums: each split covers a multiple of 32 rows
-    uint32_t splits = kSplits;
-    while (splits > 1 && B % (splits * dev::kDwRows) != 0) splits /= 2;
-    MG_CHECK(B % (splits * dev::kDwRows) == 0, MG_ERR_INVALID, "train: minibatch %u must be a multiple of 32", B);
     const uint32_t E = MG_EMBED, L = pv.layers, H = pv.hidden;
+    const bool bf = pv.precision == MG_PRECISION_BF16;
+    // 64 x 64 weight-gradient tiles over all block matrices
+    const uint32_t dw_tiles = 2 * L * (E / 64) * (H / 64);
+    // row splits of the block-matrix gradient sums: fp32, each split covers a
+    // multiple of 32 rows; bf16, a multiple of 64 rows and about two workgroups
+    // per CU in all (fewer splits, fewer partial sums to write and add)
+    const uint32_t split_rows = bf ? 16 * dev::kDwbWaves : dev::kDwRows;
+    uint32_t splits = kSplits;
+    while (splits > 1 && (B % (splits * split_rows) != 0 || (bf && dw_tiles * splits > 512))) splits /= 2;
+    MG_CHECK(B % (splits * split_rows) == 0, MG_ERR_INVALID, "train: minibatch %u must be a multiple of %u", B,
+             split_rows);
 
     {  // 1. rows
         TimedLaunch tl(MG_K_TRAIN_ROWS, st);
@@ -938,7 +1085,7 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         ra.logp_slots = logp_slots;
         ra.adv_stats = adv_stats;
         ra.head_out = head_out;
-        if (pv.precision == MG_PRECISION_BF16)
+        if (bf)
             hipLaunchKernelGGL(dev::train_rows_kernel<true>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         else
             hipLaunchKernelGGL(dev::train_rows_kernel<false>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
@@ -946,26 +1093,14 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
     }
     {  // 2. block-matrix weight gradients
         TimedLaunch tl(MG_K_TRAIN_DW, st);
-        dev::DwArgs da;
-        memset(&da, 0, sizeof(da));
-        da.rows = B;
-        da.splits = splits;
-        da.count = pv.count;
-        da.partial = ws.partial;
-        uint32_t nb = 0, tiles = 0;
-        for (uint32_t l = 0; l < L; ++l) {
-            // dUp_l[k][j] = sum_r x_l[r][k] dV_l[r][j]  (model/mlp.metal:201-203)
-            da.big[nb] = {ws.x + (size_t)l * B * E, ws.dvb + (size_t)l * B * H, E, H, E, H, pv.off_up[l], 0};
-            da.tiles_per_big[nb] = (E / 64) * (H / 64);
-            tiles += da.tiles_per_big[nb++];
-            // dDown_l[j][c] = sum_r V_l[r][j] dh_l[r][c]  (model/mlp.metal:205-207)
-            da.big[nb] = {ws.v + (size_t)l * B * H, ws.dhb + (size_t)l * B * E, H, E, H, E, pv.off_down[l], 0};
-            da.tiles_per_big[nb] = (H / 64) * (E / 64);
-            tiles += da.tiles_per_big[nb++];
+        if (bf) {
+            const auto da = dw_args<uint16_t>(pv, ws, B, splits);
+            hipLaunchKernelGGL((dev::train_dw_bf16_kernel<dev::kDwbWaves, 2>), dim3(dw_tiles * splits),
+                               dim3(64 * dev::kDwbWaves), 0, st, da);
+        } else {
+            const auto da = dw_args<float>(pv, ws, B, splits);
+            hipLaunchKernelGGL(dev::train_dw_kernel, dim3(dw_tiles * splits), dim3(256), 0, st, da);
         }
-        da.nbig = nb;
-        da.big_tiles = tiles;
-        hipLaunchKernelGGL(dev::train_dw_kernel, dim3(tiles * splits), dim3(256), 0, st, da);
         MG_HIP(hipGetLastError(), "train dW launch");
     }
     {  // 3. gradient assembly + partial norms

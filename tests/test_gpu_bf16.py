@@ -41,9 +41,14 @@ def test_bf16_forward_matches_oracle_and_differs_from_fp32(mg, orc, env):
     assert gap > 3 * err, (gap, err)
 
 
-@pytest.mark.parametrize("env,n,B,block", [("cartpole", 2048, 512, 3), ("cartpole_continuous", 2048, 1024, 1),
-                                           ("voxelnav16", 1024, 512, 2)])
-def test_bf16_minibatch(mg, orc, env, n, B, block):
+@pytest.mark.parametrize("env,n,B,block,scale", [
+    ("cartpole", 2048, 512, 3, 4),
+    ("cartpole_continuous", 2048, 1024, 1, 4),
+    ("voxelnav16", 1024, 512, 2, 4),
+    ("cartpole", 4096, 4096, 1, 4),   # weight gradients: 8 row splits of 512 rows (two load batches)
+    ("cartpole", 6144, 6144, 0, 1),   # 16 splits of 384 rows (a partial load batch)
+])
+def test_bf16_minibatch(mg, orc, env, n, B, block, scale):
     """One PPO minibatch in bf16 mode against the oracle's bf16 train step on
     the GPU's own rollout: recomputed head (median/p99/max), the Adam first
     moment (0.1 x the clipped gradient) per parameter group, post-Adam weights
@@ -54,8 +59,8 @@ def test_bf16_minibatch(mg, orc, env, n, B, block):
     eid, kernel = ENVS[env]
     T = 2
     gym = mg.Gym(kernel, n, 0)
-    model = mg.PPOModel(gym, horizon=T, minibatch=B, precision="bf16")
-    d = orc.dims(eid, bf16=True)
+    model = mg.PPOModel(gym, scale=scale, horizon=T, minibatch=B, precision="bf16")
+    d = orc.dims(eid, hidden=128 * scale, bf16=True)
     model.collect()
     s = model.download_slots()
     p0 = model.params()
@@ -70,7 +75,8 @@ def test_bf16_minibatch(mg, orc, env, n, B, block):
     assert max(errs.values()) < 1e-2, errs
     # the same gradient computed in fp32 is much further away
     P2, M2, V2 = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
-    orc.train_minibatch(orc.dims(eid), hp, P2, M2, V2, 1, *block_rows(s, n, B, block), threads=THREADS)
+    orc.train_minibatch(orc.dims(eid, hidden=128 * scale), hp, P2, M2, V2, 1, *block_rows(s, n, B, block),
+                        threads=THREADS)
     e32 = group_errors(model.pv, M2, M)
     assert e32["up0"] > 3 * errs["up0"], (e32["up0"], errs["up0"])
     assert_close(model.params(), P, TOL_TRAIN, "post-Adam weights")
