@@ -175,21 +175,23 @@ def pmc_traffic():
 def profile_pass(which):
     """Short runs of each kernel for rocprofv3 (--kernel-trace / --pmc): the
     262144-env collect and random rollout, 64 train minibatches, and one 1 GiB
-    device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters."""
+    device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters.
+    "bf16": the collect and the minibatches in bf16 mode, and the copy."""
     import metalgym_amd as mg
 
     n, T = 262144, 32
-    if which in ("collect", "all"):
+    if which in ("collect", "all", "bf16"):
+        precision = "bf16" if which == "bf16" else "fp32"
         gym = mg.Gym("rollout_cartpole", n, 0)
-        model = mg.PPOModel(gym, horizon=T)
+        model = mg.PPOModel(gym, horizon=T, precision=precision)
         for _ in range(3):
             model.collect()
-        print("profile: 3 collects of 262144 x 32", flush=True)
-        if which == "all":
+        print(f"profile: 3 {precision} collects of 262144 x 32", flush=True)
+        if which in ("all", "bf16"):
             for b in range(64):
                 mg.lib().mg_ppo_train_block(model.h, b)
             sync()
-            print("profile: 64 train minibatches of 4096 rows", flush=True)
+            print(f"profile: 64 {precision} train minibatches of 4096 rows", flush=True)
         del model, gym
     if which in ("random", "all"):
         gym = mg.Gym("rollout_cartpole", n, 0)
@@ -199,7 +201,7 @@ def profile_pass(which):
         sync()
         print("profile: 6 random rollouts of 262144 x 32", flush=True)
         del gym, bufs
-    if which in ("copy", "all"):
+    if which in ("copy", "all", "bf16"):
         nbytes = 1 << 30
         a, b = mg.DeviceBuffer(nbytes), mg.DeviceBuffer(nbytes)
         a.zero()
@@ -215,7 +217,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--profile", choices=["collect", "random", "copy", "all"], default=None,
+    ap.add_argument("--profile", choices=["collect", "random", "copy", "all", "bf16"], default=None,
                     help="run short kernel passes for rocprofv3 instead of the benchmark")
     args = ap.parse_args()
     if args.gpus != 1:
