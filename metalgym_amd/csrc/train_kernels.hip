@@ -215,6 +215,29 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, Smem&
                                           float* tp, float* scratch) {
     const int H = (int)pv.hidden, NC = H / kChunk, F = 2 * (int)pv.layers * NC;
     const typename RowsTypes<BF>::Seq seq{&pv, NC};
+    // The relu mask of chunk c: the lane's four elements of the hidden capture
+    // (rows 4 (lane / 16) .. + 3 of one column). bf16: one 8-byte load from the
+    // row-group-packed capture, a value is positive iff its bits are non-zero
+    // (relu outputs are +0 or positive).
+    static_assert(TS::RT == 1 && TS::CT == 1 && TS::MT == 16, "one 16x16 tile per wave");
+    using Mask = typename std::conditional<BF, uint2, typename TS::Acc>::type;
+    auto load_mask = [&](int c) {
+        Mask m;
+        if constexpr (BF) {
+            const int lane = threadIdx.x & 63, q = lane >> 4, col = 16 * (threadIdx.x >> 6) + (lane & 15);
+            m = *reinterpret_cast<const uint2*>(v_tile + ((size_t)(q >> 1) * H + kChunk * c + col) * 8 + 4 * (q & 1));
+        } else {
+            for_each_elem<kTR, kTW>(
+                [&](int rt, int ct, int r, int row, int col) { m[r] = v_tile[(size_t)row * H + kChunk * c + col]; });
+        }
+        return m;
+    };
+    auto positive = [](const Mask& m, int r) {
+        if constexpr (BF)
+            return (((r < 2 ? m.x : m.y) >> (16 * (r & 1))) & 0xFFFFu) != 0;
+        else
+            return m[r] > 0.0f;
+    };
     if constexpr (BF) {
         store_tile_relu_b<kTR, kTW, false>(D.h, sm.xb);
         __syncthreads();
@@ -228,22 +251,16 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, Smem&
     zero<kTR, kTW>(G.h);
     for (int c = 0; c < NC; ++c) {
         const int s = F + 2 * (((int)pv.layers - 1 - l) * NC + c);
-        // the relu mask of this chunk, loaded before the GEMM issues its weight
-        // refills (vector memory counters complete in order)
-        TS::Acc mask[TS::RT][TS::CT];
-        for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-            if constexpr (BF)  // row-group-packed
-                mask[rt][ct][r] = bf16_to_float(v_tile[((size_t)(row >> 3) * H + kChunk * c + col) * 8 + (row & 7)]);
-            else
-                mask[rt][ct][r] = v_tile[(size_t)row * H + kChunk * c + col];
-        });
+        // loaded before the GEMM issues its weight refills (vector memory
+        // counters complete in order)
+        const Mask mask = load_mask(c);
         TS::Acc v[TS::RT][TS::CT];
         zero<kTR, kTW>(v);
         if constexpr (BF) {
             uint16_t* vb = sm.vb[c & 1];  // double-buffered: no barrier before the write
             ws.template gemm<0>(v, sm.xb, s, seq);
             for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-                vb[row * kLdsB + col] = bf16_rne(mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f);
+                vb[row * kLdsB + col] = bf16_rne(positive(mask, r) ? v[rt][ct][r] : 0.0f);
             });
             __syncthreads();
             copy_tile_p8<kTNT>(vb, dv_store, H, kChunk * c);
@@ -252,7 +269,7 @@ __device__ __forceinline__ void bwd_block(const mg_policy_view& pv, int l, Smem&
             float* vs = sm.vs[c & 1];  // double-buffered: no barrier before the write
             ws.template gemm<0>(v, sm.xs, s, seq);
             for_each_elem<kTR, kTW>([&](int rt, int ct, int r, int row, int col) {
-                const float g = mask[rt][ct][r] > 0.0f ? v[rt][ct][r] : 0.0f;
+                const float g = positive(mask, r) ? v[rt][ct][r] : 0.0f;
                 dv_store[(size_t)row * H + kChunk * c + col] = g;
                 vs[row * kLds + col] = g;
             });
@@ -305,19 +322,17 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
 
     // Everything small is loaded first, so waiting for it does not wait for the
     // weight stream issued after it (vector memory counters complete in order).
+    // W_in and b_in for the embed go to the LN capture area (first written by
+    // the first LN, after every wave is done with the embed); the LN
+    // parameters (gamma, beta of every LN) are one contiguous run.
     for (int idx = tid; idx < M * O; idx += kTNT) L.obs[idx] = a.obs_slots[g0 * O + idx];
     for (int idx = tid; idx < kEmbed * HD; idx += kTNT) L.wh[idx] = pv.params[pv.off_head + idx];
-    // W_in and b_in for the embed, in the LN capture area (first written by the
-    // first LN, after every wave is done with the embed)
     float* winL = L.xn;
     float* binL = L.xn + kMaxObsT * kEmbed;
     static_assert((kMaxObsT + 1) * kEmbed <= (MG_MAX_LAYERS + 1) * kTR * kEmbed, "embed staging fits");
     for (int idx = tid; idx < O * kEmbed; idx += kTNT) winL[idx] = pv.params[pv.off_in_w + idx];
     if (tid < kEmbed) binL[tid] = pv.params[pv.off_in_b + tid];
-    for (int idx = tid; idx < (NL + 1) * 2 * kEmbed; idx += kTNT) {
-        const int ln = idx / (2 * kEmbed), k = idx % (2 * kEmbed);
-        L.ln[idx] = k < kEmbed ? pv.params[pv.off_ln_gamma[ln] + k] : pv.params[pv.off_ln_beta[ln] + k - kEmbed];
-    }
+    for (int idx = tid; idx < (NL + 1) * 2 * kEmbed; idx += kTNT) L.ln[idx] = pv.params[pv.off_ln_gamma[0] + idx];
     // the loss inputs of this thread's row (32 threads per row)
     const int lrow = tid >> 5, lk = tid & 31;
     float an, oldLp, ret;
@@ -685,48 +700,77 @@ struct ReduceArgs {
     float inv_rows;
 };
 
-__global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
-    constexpr int NG = 256 / kRedCols;  // thread groups per column
+// Workgroup wg of nwg summing tile-partial columns (kRedCols at a time): NT /
+// kRedCols thread groups per column each add a range of tiles, and the ranges
+// are added in order. Writes the vector / head gradient and the minibatch
+// LossStats; returns this thread's sum of the squared gradient values it
+// wrote. NT threads.
+template <int NT>
+__device__ __forceinline__ float reduce_tile_partials(const ReduceArgs& a, uint32_t wg, uint32_t nwg) {
+    constexpr int NG = NT / kRedCols;  // thread groups per column
     __shared__ float part[NG][kRedCols];
-    __shared__ float red[4];
+    const int t = threadIdx.x;
+    float sq = 0.0f;
+    const uint32_t grp = t / kRedCols;
+    const uint32_t lo = grp * a.tiles / NG, hi = (grp + 1) * a.tiles / NG;
+    const uint32_t stat0 = a.float_group + a.head_count;
+    for (uint32_t c0 = wg * kRedCols; c0 < stat0 + 5; c0 += nwg * kRedCols) {
+        const uint32_t col = c0 + t % kRedCols;
+        float s = 0.0f;
+        if (col < stat0 + 5) {
+            const float* src = a.tp + col;
+            // loads issued eight at a time, added in tile order
+            for (uint32_t k0 = lo; k0 < hi; k0 += 8) {
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) x[u] = k0 + u < hi ? src[(size_t)(k0 + u) * a.tp_count] : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += x[u];
+            }
+        }
+        part[grp][t % kRedCols] = s;
+        __syncthreads();
+        if (t < kRedCols && col < stat0 + 5) {
+            float g = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NG; ++q) g += part[q][t];
+            if (col < a.float_group) {
+                a.grad[col] = g;
+                sq += g * g;
+            } else if (col < stat0) {
+                a.grad[a.off_head + (col - a.float_group)] = g;
+                sq += g * g;
+            } else {
+                a.mb_stats[col - stat0] = g * a.inv_rows;  // model/ppo.h:925-943 means
+            }
+        }
+        __syncthreads();
+    }
+    return sq;
+}
+
+// The workgroup's sum of sq to *out, in a fixed order (a DPP tree within each
+// wave, then the NW waves in order).
+template <int NW>
+__device__ __forceinline__ void write_norm_part(float sq, float* out) {
+    __shared__ float red[NW];
+    sq = group_sum<64>(sq);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = red[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) s += red[w];
+        *out = s;
+    }
+}
+
+__global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
     const int t = threadIdx.x;
     float sq = 0.0f;
     if (blockIdx.x < a.small_wgs) {
-        const uint32_t grp = t / kRedCols;
-        const uint32_t lo = grp * a.tiles / NG, hi = (grp + 1) * a.tiles / NG;
-        const uint32_t stat0 = a.float_group + a.head_count;
-        for (uint32_t c0 = blockIdx.x * kRedCols; c0 < stat0 + 5; c0 += a.small_wgs * kRedCols) {
-            const uint32_t col = c0 + t % kRedCols;
-            float s = 0.0f;
-            if (col < stat0 + 5) {
-                const float* src = a.tp + col;
-                // loads issued eight at a time, added in tile order
-                for (uint32_t k0 = lo; k0 < hi; k0 += 8) {
-                    float x[8];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) x[u] = k0 + u < hi ? src[(size_t)(k0 + u) * a.tp_count] : 0.0f;
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) s += x[u];
-                }
-            }
-            part[grp][t % kRedCols] = s;
-            __syncthreads();
-            if (t < kRedCols && col < stat0 + 5) {
-                float g = 0.0f;
-#pragma unroll
-                for (int q = 0; q < NG; ++q) g += part[q][t];
-                if (col < a.float_group) {
-                    a.grad[col] = g;
-                    sq += g * g;
-                } else if (col < stat0) {
-                    a.grad[a.off_head + (col - a.float_group)] = g;
-                    sq += g * g;
-                } else {
-                    a.mb_stats[col - stat0] = g * a.inv_rows;  // model/ppo.h:925-943 means
-                }
-            }
-            __syncthreads();
-        }
+        sq = reduce_tile_partials<256>(a, blockIdx.x, a.small_wgs);
     } else {
         const uint32_t nw = gridDim.x - a.small_wgs;
         for (uint32_t i = a.float_group + (blockIdx.x - a.small_wgs) * 256 + t; i < a.off_head; i += nw * 256) {
@@ -740,12 +784,92 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
             sq += g * g;
         }
     }
-    sq = group_sum<64>(sq);
-    __syncthreads();
-    if ((t & 63) == 0) red[t >> 6] = sq;
-    __syncthreads();
-    if (t == 0) a.normpart[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+    write_norm_part<4>(sq, a.normpart + blockIdx.x);
 }
+
+// bf16 weight gradients, tile partial sums and partial norms in one launch
+// (replacing train_dw + grad_reduce when the block matrices have enough 32 x
+// 32 tiles to fill the GPU without row splits). Workgroup t computes tile t
+// of the block matrices over all rows, operands as in train_dw_bf16_kernel:
+// its NW waves take every NW-th 16-row step and add their tiles in LDS in
+// wave order, and the tile goes straight to grad. Each wave keeps up to 2 U
+// steps of loads in flight. Then the workgroups share the tile-partial
+// columns (reduce_tile_partials). Every
+// workgroup writes the squared norm of what it wrote to normpart; the entries
+// past the grid are zeroed, so the Adam kernel's fixed-order sum over
+// kReduceBlocks entries is the same sum. (At 4096 rows, 2 blocks, hidden 512:
+// 16 waves with U = 4 or 2 and 8 waves with U = 4 ran within 3% of each other.
+// The kernel moves ≈50 MB between L2 and the fabric, more than the 20 MB of
+// captures: each XCD fetches the capture blocks its tiles share. Against the
+// split kernel plus grad_reduce it saves one launch per minibatch.)
+struct DwFusedArgs {
+    DwArgsT<uint16_t> dw;
+    ReduceArgs red;
+};
+template <int NW, int U>
+__global__ void __launch_bounds__(64 * NW) train_dw_bf16_fused_kernel(const DwFusedArgs a) {
+    __shared__ float red[NW][32 * 32];
+    float sq = 0.0f;
+    {
+        uint32_t t = blockIdx.x, m = 0;
+        while (t >= a.dw.tiles_per_big[m]) t -= a.dw.tiles_per_big[m], ++m;
+        const BigMatT<uint16_t>& bm = a.dw.big[m];
+        // the hidden-side tile index varies fastest: workgroups go to the 8 XCDs
+        // round robin (and every matrix has a multiple of 8 tiles), so XCD k
+        // computes the tiles of hidden blocks k and k + 8 for every embed block
+        // and each capture block is fetched into its L2 by as few XCDs as can
+        const uint32_t ntm = bm.mdim / 32, ntn = bm.ndim / 32;
+        const uint32_t tm = bm.mdim > bm.ndim ? t % ntm : t / ntn;
+        const uint32_t tn = bm.mdim > bm.ndim ? t / ntm : t % ntn;
+        const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        // lane's operands in step s: row group 2 (NW s + w) + lane / 32, column
+        // tile + lane % 32
+        const size_t g0 = 2 * w + (lane >> 5);
+        const uint16_t* xp = bm.x + (g0 * bm.ldx + tm * 32 + (lane & 31)) * 8;
+        const uint16_t* yp = bm.y + (g0 * bm.ldy + tn * 32 + (lane & 31)) * 8;
+        const size_t xstep = (size_t)16 * NW * bm.ldx, ystep = (size_t)16 * NW * bm.ldy;  // 2 NW row groups
+        const uint32_t steps = a.dw.rows / (16 * NW);  // rows: a multiple of 16 NW
+        const uint32_t batches = (steps + U - 1) / U;
+        auto load = [&](u32x4 (&op)[U][2], uint32_t b) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t st = b * U + u;
+                if (st < steps) {
+                    op[u][0] = *reinterpret_cast<const u32x4*>(xp + st * xstep);
+                    op[u][1] = *reinterpret_cast<const u32x4*>(yp + st * ystep);
+                } else {
+                    op[u][0] = op[u][1] = u32x4{0, 0, 0, 0};
+                }
+            }
+        };
+        f32x16 acc = f32x16{};
+        u32x4 cur[U][2], nxt[U][2];
+        load(cur, 0);
+        for (uint32_t b = 0; b < batches; ++b) {
+            if (b + 1 < batches) load(nxt, b + 1);
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc = ShapeB<32>::mfma(cur[u][0], cur[u][1], acc);
+#pragma unroll
+            for (int u = 0; u < U; ++u) cur[u][0] = nxt[u][0], cur[u][1] = nxt[u][1];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[w][c32_row(r, lane) * 32 + (lane & 31)] = acc[r];
+        __syncthreads();
+        float* out = a.red.grad + bm.off + (size_t)tm * 32 * bm.ndim + tn * 32;
+        for (int e = threadIdx.x; e < 32 * 32; e += 64 * NW) {
+            float v = red[0][e];
+#pragma unroll
+            for (int q = 1; q < NW; ++q) v += red[q][e];
+            out[(size_t)(e >> 5) * bm.ndim + (e & 31)] = v;
+            sq += v * v;
+        }
+    }
+    sq += reduce_tile_partials<64 * NW>(a.red, blockIdx.x, gridDim.x);
+    write_norm_part<NW>(sq, a.red.normpart + blockIdx.x);
+    if (blockIdx.x == 0)
+        for (uint32_t i = gridDim.x + threadIdx.x; i < (uint32_t)kReduceBlocks; i += 64 * NW) a.red.normpart[i] = 0.0f;
+}
+constexpr int kDwfWaves = 8;
 
 // The block matrices are contiguous from float_group: per block up [128 x H]
 // then down [H x 128]. Both matrix kinds split into (128 x H) / 1024 tiles of
@@ -1006,6 +1130,9 @@ int check_matrix_layout(const mg_policy_view& pv) {
         MG_CHECK(pv.off_up[l] == pv.float_group + 2 * l * E * H && pv.off_down[l] == pv.off_up[l] + E * H &&
                      pv.off_head == pv.float_group + 2 * pv.layers * E * H,
                  MG_ERR_INVALID, "policy: block matrices must be contiguous from float_group");
+    for (uint32_t l = 0; l <= pv.layers; ++l)
+        MG_CHECK(pv.off_ln_gamma[l] == pv.off_ln_gamma[0] + 2 * l * E && pv.off_ln_beta[l] == pv.off_ln_gamma[l] + E,
+                 MG_ERR_INVALID, "policy: LN parameters must be contiguous (gamma, beta per LN)");
     return MG_OK;
 }
 
@@ -1020,9 +1147,9 @@ int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv) {
 }
 
 // The weight-gradient jobs of one minibatch: per block, dUp and dDown from
-// the captures (T: their element type); 64 x 64 tiles.
+// the captures (T: their element type); tile x tile tiles.
 template <class T>
-dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B, uint32_t splits) {
+dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B, uint32_t splits, uint32_t tile) {
     const uint32_t E = MG_EMBED, H = pv.hidden;
     const T* x = reinterpret_cast<const T*>(ws.x);
     const T* v = reinterpret_cast<const T*>(ws.v);
@@ -1038,11 +1165,11 @@ dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B,
     for (uint32_t l = 0; l < pv.layers; ++l) {
         // dUp_l[k][j] = sum_r x_l[r][k] dV_l[r][j]  (model/mlp.metal:201-203)
         da.big[nb] = {x + (size_t)l * B * E, dv + (size_t)l * B * H, E, H, E, H, pv.off_up[l], 0};
-        da.tiles_per_big[nb] = (E / 64) * (H / 64);
+        da.tiles_per_big[nb] = (E / tile) * (H / tile);
         tiles += da.tiles_per_big[nb++];
         // dDown_l[j][c] = sum_r V_l[r][j] dh_l[r][c]  (model/mlp.metal:205-207)
         da.big[nb] = {v + (size_t)l * B * H, dh + (size_t)l * B * E, H, E, H, E, pv.off_down[l], 0};
-        da.tiles_per_big[nb] = (H / 64) * (E / 64);
+        da.tiles_per_big[nb] = (H / tile) * (E / tile);
         tiles += da.tiles_per_big[nb++];
     }
     da.nbig = nb;
@@ -1091,39 +1218,52 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
             hipLaunchKernelGGL(dev::train_rows_kernel<false>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         MG_HIP(hipGetLastError(), "train rows launch");
     }
-    {  // 2. block-matrix weight gradients
+    dev::ReduceArgs ga;
+    ga.partial = ws.partial;
+    ga.tp = ws.tp;
+    ga.grad = ws.grad;
+    ga.normpart = ws.normpart;
+    ga.splits = splits;
+    ga.tiles = B / kTileRows;
+    ga.tp_count = ws.tp_count;
+    ga.count = pv.count;
+    ga.float_group = pv.float_group;
+    ga.off_head = pv.off_head;
+    ga.head_count = E * pv.head_dim;
+    ga.mb_stats = mb_stats;
+    ga.inv_rows = 1.0f / (float)B;
+    // kRedCols tile-partial columns per small workgroup, at most half the grid
+    const uint32_t cols = pv.float_group + E * pv.head_dim + 5, cw = dev::kRedCols;
+    ga.small_wgs = (cols + cw - 1) / cw < kReduceBlocks / 2 ? (cols + cw - 1) / cw : kReduceBlocks / 2;
+    // bf16 with 128 to 1024 tiles of 32 x 32: weight gradients without row
+    // splits, fused with the tile-partial sums (one launch instead of two)
+    const uint32_t tiles32 = 2 * L * (E / 32) * (H / 32);
+    if (bf && tiles32 >= 128 && tiles32 <= (uint32_t)kReduceBlocks && B % (16 * dev::kDwfWaves) == 0) {
         TimedLaunch tl(MG_K_TRAIN_DW, st);
-        if (bf) {
-            const auto da = dw_args<uint16_t>(pv, ws, B, splits);
-            hipLaunchKernelGGL((dev::train_dw_bf16_kernel<dev::kDwbWaves, 2>), dim3(dw_tiles * splits),
-                               dim3(64 * dev::kDwbWaves), 0, st, da);
-        } else {
-            const auto da = dw_args<float>(pv, ws, B, splits);
-            hipLaunchKernelGGL(dev::train_dw_kernel, dim3(dw_tiles * splits), dim3(256), 0, st, da);
-        }
+        dev::DwFusedArgs fa;
+        fa.dw = dw_args<uint16_t>(pv, ws, B, 1, 32);
+        fa.red = ga;
+        hipLaunchKernelGGL((dev::train_dw_bf16_fused_kernel<dev::kDwfWaves, 4>), dim3(tiles32),
+                           dim3(64 * dev::kDwfWaves), 0, st, fa);
         MG_HIP(hipGetLastError(), "train dW launch");
-    }
-    {  // 3. gradient assembly + partial norms
-        TimedLaunch tl(MG_K_GRAD_REDUCE, st);
-        dev::ReduceArgs ga;
-        ga.partial = ws.partial;
-        ga.tp = ws.tp;
-        ga.grad = ws.grad;
-        ga.normpart = ws.normpart;
-        ga.splits = splits;
-        ga.tiles = B / kTileRows;
-        ga.tp_count = ws.tp_count;
-        ga.count = pv.count;
-        ga.float_group = pv.float_group;
-        ga.off_head = pv.off_head;
-        ga.head_count = E * pv.head_dim;
-        ga.mb_stats = mb_stats;
-        ga.inv_rows = 1.0f / (float)B;
-        // kRedCols tile-partial columns per small workgroup, at most half the grid
-        const uint32_t cols = pv.float_group + E * pv.head_dim + 5, cw = dev::kRedCols;
-        ga.small_wgs = (cols + cw - 1) / cw < kReduceBlocks / 2 ? (cols + cw - 1) / cw : kReduceBlocks / 2;
-        hipLaunchKernelGGL(dev::grad_reduce_kernel, dim3(kReduceBlocks), dim3(256), 0, st, ga);
-        MG_HIP(hipGetLastError(), "grad reduce launch");
+    } else {
+        {  // 2. block-matrix weight gradients
+            TimedLaunch tl(MG_K_TRAIN_DW, st);
+            if (bf) {
+                const auto da = dw_args<uint16_t>(pv, ws, B, splits, 64);
+                hipLaunchKernelGGL((dev::train_dw_bf16_kernel<dev::kDwbWaves, 2>), dim3(dw_tiles * splits),
+                                   dim3(64 * dev::kDwbWaves), 0, st, da);
+            } else {
+                const auto da = dw_args<float>(pv, ws, B, splits, 64);
+                hipLaunchKernelGGL(dev::train_dw_kernel, dim3(dw_tiles * splits), dim3(256), 0, st, da);
+            }
+            MG_HIP(hipGetLastError(), "train dW launch");
+        }
+        {  // 3. gradient assembly + partial norms
+            TimedLaunch tl(MG_K_GRAD_REDUCE, st);
+            hipLaunchKernelGGL(dev::grad_reduce_kernel, dim3(kReduceBlocks), dim3(256), 0, st, ga);
+            MG_HIP(hipGetLastError(), "grad reduce launch");
+        }
     }
     {  // 4. Adam
         TimedLaunch tl(MG_K_ADAM, st);
