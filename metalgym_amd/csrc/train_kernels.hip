@@ -324,15 +324,33 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     // weight stream issued after it (vector memory counters complete in order).
     // W_in and b_in for the embed go to the LN capture area (first written by
     // the first LN, after every wave is done with the embed); the LN
-    // parameters (gamma, beta of every LN) are one contiguous run.
-    for (int idx = tid; idx < M * O; idx += kTNT) L.obs[idx] = a.obs_slots[g0 * O + idx];
-    for (int idx = tid; idx < kEmbed * HD; idx += kTNT) L.wh[idx] = pv.params[pv.off_head + idx];
+    // parameters (gamma, beta of every LN) are one contiguous run. The first
+    // element per thread of each array (and two of the LN run: all of it up to
+    // 3 LNs) is loaded before any is stored, so their memory latencies overlap;
+    // larger shapes finish in loops.
     float* winL = L.xn;
     float* binL = L.xn + kMaxObsT * kEmbed;
     static_assert((kMaxObsT + 1) * kEmbed <= (MG_MAX_LAYERS + 1) * kTR * kEmbed, "embed staging fits");
-    for (int idx = tid; idx < O * kEmbed; idx += kTNT) winL[idx] = pv.params[pv.off_in_w + idx];
-    if (tid < kEmbed) binL[tid] = pv.params[pv.off_in_b + tid];
-    for (int idx = tid; idx < (NL + 1) * 2 * kEmbed; idx += kTNT) L.ln[idx] = pv.params[pv.off_ln_gamma[0] + idx];
+    const float* lnp = pv.params + pv.off_ln_gamma[0];
+    const int n_obs = M * O, n_wh = kEmbed * HD, n_win = O * kEmbed, n_ln = (NL + 1) * 2 * kEmbed;
+    {
+        const float o0 = tid < n_obs ? a.obs_slots[g0 * O + tid] : 0.0f;
+        const float h0 = tid < n_wh ? pv.params[pv.off_head + tid] : 0.0f;
+        const float w0 = tid < n_win ? pv.params[pv.off_in_w + tid] : 0.0f;
+        const float b0 = tid < kEmbed ? pv.params[pv.off_in_b + tid] : 0.0f;
+        const float l0 = tid < n_ln ? lnp[tid] : 0.0f;
+        const float l1 = tid + kTNT < n_ln ? lnp[tid + kTNT] : 0.0f;
+        if (tid < n_obs) L.obs[tid] = o0;
+        if (tid < n_wh) L.wh[tid] = h0;
+        if (tid < n_win) winL[tid] = w0;
+        if (tid < kEmbed) binL[tid] = b0;
+        if (tid < n_ln) L.ln[tid] = l0;
+        if (tid + kTNT < n_ln) L.ln[tid + kTNT] = l1;
+    }
+    for (int idx = tid + kTNT; idx < n_obs; idx += kTNT) L.obs[idx] = a.obs_slots[g0 * O + idx];
+    for (int idx = tid + kTNT; idx < n_wh; idx += kTNT) L.wh[idx] = pv.params[pv.off_head + idx];
+    for (int idx = tid + kTNT; idx < n_win; idx += kTNT) winL[idx] = pv.params[pv.off_in_w + idx];
+    for (int idx = tid + 2 * kTNT; idx < n_ln; idx += kTNT) L.ln[idx] = lnp[idx];
     // the loss inputs of this thread's row (32 threads per row)
     const int lrow = tid >> 5, lk = tid & 31;
     float an, oldLp, ret;
