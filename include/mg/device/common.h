@@ -40,10 +40,20 @@ __device__ __forceinline__ float dpp_lane(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
+// v of lane L (a scalar read; every lane of the wave must be active).
+template <int L>
+__device__ __forceinline__ float lane_value(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), L));
+}
+
 // Sum over groups of G consecutive lanes (G a power of two <= 64); every lane
 // of a group gets the same bits. Inside a 16-lane row the partners come from
 // DPP moves (quad_perm xor 1, xor 2, then the half-row and row mirrors, each
-// pairing the group's halves); wider groups add one lane shuffle per doubling.
+// pairing the group's halves). Across rows the four row sums are read as
+// scalars (v_readlane, no LDS round trip) and added pairwise: rows 0 + 1 and
+// 2 + 3 for G = 32, then those two for G = 64 (the same sums, in the same
+// order up to commutation, as shuffling lanes l ^ 16 and l ^ 32). Every lane
+// of the wave must be active.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
     static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "power-of-two group");
@@ -51,8 +61,13 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 4) v += dpp_lane<0x4E>(v);   // quad_perm [2, 3, 0, 1]
     if constexpr (G >= 8) v += dpp_lane<0x141>(v);  // row_half_mirror
     if constexpr (G >= 16) v += dpp_lane<0x140>(v); // row_mirror
-    if constexpr (G >= 32) v += __shfl_xor(v, 16, kWave);
-    if constexpr (G >= 64) v += __shfl_xor(v, 32, kWave);
+    if constexpr (G >= 32) {
+        const float lo = lane_value<0>(v) + lane_value<16>(v), hi = lane_value<32>(v) + lane_value<48>(v);
+        if constexpr (G == 32)
+            v = (threadIdx.x & 32) ? hi : lo;
+        else
+            v = lo + hi;
+    }
     return v;
 }
 
@@ -64,8 +79,14 @@ __device__ __forceinline__ float group_max(float v) {
     if constexpr (G >= 4) v = fmaxf(v, dpp_lane<0x4E>(v));
     if constexpr (G >= 8) v = fmaxf(v, dpp_lane<0x141>(v));
     if constexpr (G >= 16) v = fmaxf(v, dpp_lane<0x140>(v));
-    if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16, kWave));
-    if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, kWave));
+    if constexpr (G >= 32) {
+        const float lo = fmaxf(lane_value<0>(v), lane_value<16>(v));
+        const float hi = fmaxf(lane_value<32>(v), lane_value<48>(v));
+        if constexpr (G == 32)
+            v = (threadIdx.x & 32) ? hi : lo;
+        else
+            v = fmaxf(lo, hi);
+    }
     return v;
 }
 

@@ -73,6 +73,14 @@ __device__ __forceinline__ void tile_colsum2(const float* b, const float* a, flo
     }
 }
 
+// The loss's transcendentals on the hardware units: e^x = 2^(x log2 e) and
+// ln x = log2(x) ln 2 (v_exp_f32 / v_log_f32, about 1 ulp plus the rounding of
+// the scaling). The loss and its gradient are compared with the oracle within
+// tolerance, not bit for bit, so they do not need the bit-reproducible
+// software versions the samplers use.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+__device__ __forceinline__ float fast_log(float x) { return __builtin_amdgcn_logf(x) * 0.693147180559945309f; }
+
 struct RowsArgs {
     mg_policy_view pv;
     TrainWs ws;
@@ -409,12 +417,12 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
         if (!pv.continuous) {  // model/policy.metal:14-69
             const float z0 = v0 ? h[j0] : -__builtin_huge_valf(), z1 = v1 ? h[j1] : -__builtin_huge_valf();
             const float rowMax = group_max<32>(fmaxf(z0, z1));
-            float e = v0 ? mg::expf(z0 - rowMax) : 0.0f;
-            if (v1) e += mg::expf(z1 - rowMax);
-            const float lse = rowMax + mg::logf(group_sum<32>(e));
+            float e = v0 ? fast_exp(z0 - rowMax) : 0.0f;
+            if (v1) e += fast_exp(z1 - rowMax);
+            const float lse = rowMax + fast_log(group_sum<32>(e));
             float ent = 0.0f;
-            if (v0) lp0 = z0 - lse, p0 = mg::expf(lp0), ent -= p0 * lp0;
-            if (v1) lp1 = z1 - lse, p1 = mg::expf(lp1), ent -= p1 * lp1;
+            if (v0) lp0 = z0 - lse, p0 = fast_exp(lp0), ent -= p0 * lp0;
+            if (v1) lp1 = z1 - lse, p1 = fast_exp(lp1), ent -= p1 * lp1;
             entropy = group_sum<32>(ent);
             logpA = h[act] - lse;
         } else {  // model/gaussian.metal:76-135
@@ -423,14 +431,14 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
             float lp = 0.0f, ent = 0.0f;
             if (v0) {
                 const float ls = logStd[j0];
-                is0 = mg::expf(-ls);
+                is0 = fast_exp(-ls);
                 d0 = (actg[j0] - h[j0]) * is0;
                 lp += -0.5f * d0 * d0 - ls - kLogSqrt2Pi;
                 ent += ls + kLogSqrt2Pi + 0.5f;
             }
             if (v1) {
                 const float ls = logStd[j1];
-                is1 = mg::expf(-ls);
+                is1 = fast_exp(-ls);
                 d1 = (actg[j1] - h[j1]) * is1;
                 lp += -0.5f * d1 * d1 - ls - kLogSqrt2Pi;
                 ent += ls + kLogSqrt2Pi + 0.5f;
@@ -438,7 +446,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
             logpA = group_sum<32>(lp);
             entropy = group_sum<32>(ent);
         }
-        const float ratio = mg::expf(logpA - oldLp);
+        const float ratio = fast_exp(logpA - oldLp);
         const float surr1 = ratio * an;
         const float cr = fminf(fmaxf(ratio, 1.0f - clip), 1.0f + clip);
         const float surr2 = cr * an;
