@@ -7,7 +7,9 @@
 //                   t == T: write the bootstrap head (model/ppo.h:735)
 //
 // Env lanes are threads 0..M-1 (one wave). A small State lives in registers of
-// its lane for the whole rollout; a large one is updated in place. Per env and
+// its lane for the whole rollout; a larger one is staged in LDS for the T steps
+// when the tile's envs fit beside the forward's LDS (copied in and out by the
+// whole workgroup), else it is updated in place in device memory. Per env and
 // step the RNG order is: sample draw(s), reset draws if done, then step
 // (model/ppo.h:728-730, rollout.h:46-47).
 #pragma once
@@ -37,6 +39,25 @@ struct CollectSmem {
     float head[M * HD];
 };
 
+// LDS staging of a State too large for registers: the tile's M states at an
+// odd stride of dwords (env e at dword e * STRIDE), so the lanes' accesses to
+// one field fall in different banks. Used when the states fit beside the
+// forward's LDS at the kernel's workgroups per CU; gathers from a state (a
+// VoxelNav heightmap's ray march) then cost an LDS round trip instead of a
+// cache miss.
+template <typename Env, int M, bool BF16>
+struct LdsState {
+    using State = typename Env::State;
+    static constexpr uint32_t SD = sizeof(State) / 4;           // dwords per state
+    static constexpr uint32_t STRIDE = SD % 2 ? SD : SD + 1;   // odd dword stride
+    static constexpr size_t BYTES = (size_t)M * STRIDE * 4;
+    static constexpr int O = Env::OBS_DIM, HD = Env::ACT_DIM + 1;
+    static constexpr bool USE = !EnvTraits<Env>::STATE_IN_REGISTERS && sizeof(State) % 4 == 0 &&
+                                alignof(State) <= 4 &&
+                                sizeof(CollectSmem<M, O, HD, BF16>) + BYTES <=
+                                    (size_t)163840 / CollectShape<M, O>::MIN_WG;
+};
+
 // BF16: the policy forward multiplies bfloat16 operands (policy_bf16.h).
 template <typename Env, int M, bool BF16>
 __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectShape<M, Env::OBS_DIM>::MIN_WG))
@@ -46,8 +67,10 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     using Action = typename Env::Action;
     using Obs = typename Env::Obs;
     using CS = CollectShape<M, Env::OBS_DIM>;
+    using LS = LdsState<Env, M, BF16>;
     constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
     __shared__ CollectSmem<M, O, HD, BF16> sm;
+    __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     FwdRegs<M, CS::W> R;
 
     const int tid = threadIdx.x;
@@ -60,14 +83,24 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
 
     uint32_t rng = 0;
     uint8_t done = 0;
-    // A small State lives in this register copy; a large one is used in place.
+    // A small State lives in this register copy; a larger one in LDS or, if it
+    // does not fit there, in place in device memory.
     std::conditional_t<Tr::STATE_IN_REGISTERS, State, char> sreg;
     auto S = [&]() -> State& {
         if constexpr (Tr::STATE_IN_REGISTERS)
             return sreg;
+        else if constexpr (LS::USE)
+            return *reinterpret_cast<State*>(lds_state + tid * LS::STRIDE);
         else
             return states[i];
     };
+    if constexpr (LS::USE) {
+        // the tile's states are contiguous in device memory: dword k of the run
+        // is dword k % SD of env k / SD
+        const uint32_t* gin = reinterpret_cast<const uint32_t*>(states + (size_t)blockIdx.x * M);
+        for (uint32_t k = tid; k < M * LS::SD; k += CS::NT) lds_state[(k / LS::SD) * LS::STRIDE + k % LS::SD] = gin[k];
+        __syncthreads();
+    }
     float obs[O];
 
     if (envLane) {
@@ -135,6 +168,10 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
         if constexpr (Tr::STATE_IN_REGISTERS) states[i] = sreg;
         a.rng[i] = rng;
         a.done[i] = done;
+    }
+    if constexpr (LS::USE) {  // every env lane's last step is before the loop's final barrier
+        uint32_t* gout = reinterpret_cast<uint32_t*>(states + (size_t)blockIdx.x * M);
+        for (uint32_t k = tid; k < M * LS::SD; k += CS::NT) gout[k] = lds_state[(k / LS::SD) * LS::STRIDE + k % LS::SD];
     }
 }
 
