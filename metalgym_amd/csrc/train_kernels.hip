@@ -1,9 +1,10 @@
-// One PPO minibatch update (model/ppo.h:906-916) as four launches:
+// One PPO minibatch update (model/ppo.h:906-916) as four launches (three in
+// bf16 mode at the usual shapes, where 2 and 3 are one kernel):
 //
 //  1. train_rows: per 16-row tile (256 workgroups for 4096 rows), the forward
 //     recompute with activation capture (model/ppo.h:909), the loss and head
 //     gradient (model/policy.metal:14-69 / model/gaussian.metal:76-135) and the
-//     whole backward dX chain (model/ppo.h:793-865) on fp32 MFMA, writing the
+//     whole backward dX chain (model/ppo.h:793-865) on MFMA, writing the
 //     activations and gradients the weight gradients need.
 //     The same workgroup writes its tile's sums of the vector-parameter, head
 //     and log_std gradients and of the loss statistics.
@@ -13,6 +14,9 @@
 //  3. grad_reduce: sums the tile partials and the row splits in fixed order,
 //     writes the minibatch's LossStats (model/ppo.h:925-943) and one partial
 //     squared norm per workgroup.
+//     (bf16 with 128 to 1024 tiles of 32 x 32: train_dw_bf16_fused computes
+//     the weight gradients without row splits and does this step's tile sums
+//     and partial norms in the same launch.)
 //  4. adam: every workgroup adds the partial norms in the same fixed order
 //     (so no cross-workgroup synchronisation is needed), applies the clip
 //     scale and Adam (model/optimizer.metal:23-60).
