@@ -164,6 +164,48 @@ def cpu_baseline(target_s=10.0):
                       f"{threads} threads, {dt:.1f} s"}
 
 
+def cpu_extras(threads=None):
+    """The oracle on the host for the other BASELINE configurations, bounded:
+    the random rollout at 262144 envs (config 1), and the full PPO loop at 4096
+    envs (config 3) from one collect and a few timed minibatches, an iteration
+    being one collect plus 4 epochs x 32 minibatches of 4096 rows."""
+    import numpy as np
+
+    import oracle as orc
+
+    threads = threads or max(1, min(16, os.cpu_count() or 1))
+    T = 32
+    out = {}
+    n = 262144
+    g = orc.GymState(orc.CARTPOLE, n, 0)
+    t0 = time.perf_counter()
+    orc.rollout(g, T, random=True, threads=threads)
+    dt = time.perf_counter() - t0
+    out["cpu_random_262144"] = {"env_steps_per_s": n * T / dt, "cores": threads, "kind": "port",
+                                "sample": f"oracle random rollout of 262144 CartPole envs x 32, {dt:.1f} s"}
+    n, k = 4096, 2
+    d = orc.dims(orc.CARTPOLE)
+    params = orc.init_params(d, 0)
+    g = orc.GymState(orc.CARTPOLE, n, 0)
+    slots = orc.Slots(orc.CARTPOLE, n, T)
+    t0 = time.perf_counter()
+    orc.collect(g, d, params, T, slots, first=True, threads=threads)
+    tc = time.perf_counter() - t0
+    hp = orc.hparams()
+    P, M, V = params.copy(), np.zeros_like(params), np.zeros_like(params)
+    t0 = time.perf_counter()
+    for step in range(1, k + 1):
+        t = step - 1
+        orc.train_minibatch(d, hp, P, M, V, step, slots.obs[t], slots.actions[t], slots.adv[t], slots.ret[t],
+                            slots.logp[t], threads=threads)
+    tm = (time.perf_counter() - t0) / k
+    it = tc + 4 * T * tm
+    out["cpu_full_ppo_4096"] = {"env_steps_per_s": n * T / it, "cores": threads, "kind": "port",
+                                "sample": f"oracle collect of 4096 envs x 32 ({tc:.1f} s) and {k} minibatches of "
+                                          f"4096 rows ({tm:.2f} s each); iteration = collect + 128 minibatches"}
+    return out
+
+
 def pmc_traffic():
     """HBM bytes per collect launch from the committed rocprofv3 --pmc summary, if any."""
     p = os.path.join(ROOT, "profiles", "collect_cartpole_262144_pmc.json")
@@ -306,6 +348,8 @@ def main():
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        if "extra" in line:
+            line["extra"].update(cpu_extras())
     print(json.dumps(line), flush=True)
 
 
