@@ -176,33 +176,43 @@ def cpu_extras(threads=None):
     threads = threads or max(1, min(16, os.cpu_count() or 1))
     T = 32
     out = {}
+
+    def repeated(fn, min_s=2.0):
+        """Calls fn until min_s seconds have passed; returns (calls, seconds)."""
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            fn(calls)
+            calls += 1
+            dt = time.perf_counter() - t0
+            if dt >= min_s:
+                return calls, dt
+
     n = 262144
     g = orc.GymState(orc.CARTPOLE, n, 0)
-    t0 = time.perf_counter()
-    orc.rollout(g, T, random=True, threads=threads)
-    dt = time.perf_counter() - t0
-    out["cpu_random_262144"] = {"env_steps_per_s": n * T / dt, "cores": threads, "kind": "port",
-                                "sample": f"oracle random rollout of 262144 CartPole envs x 32, {dt:.1f} s"}
-    n, k = 4096, 2
+    reps, dt = repeated(lambda _: orc.rollout(g, T, random=True, threads=threads))
+    out["cpu_random_262144"] = {"env_steps_per_s": reps * n * T / dt, "cores": threads, "kind": "port",
+                                "sample": f"oracle random rollouts of 262144 CartPole envs x 32, {reps} in {dt:.1f} s"}
+    n = 4096
     d = orc.dims(orc.CARTPOLE)
     params = orc.init_params(d, 0)
     g = orc.GymState(orc.CARTPOLE, n, 0)
     slots = orc.Slots(orc.CARTPOLE, n, T)
-    t0 = time.perf_counter()
-    orc.collect(g, d, params, T, slots, first=True, threads=threads)
-    tc = time.perf_counter() - t0
+    nc, dc = repeated(lambda c: orc.collect(g, d, params, T, slots, first=(c == 0), threads=threads))
+    tc = dc / nc
     hp = orc.hparams()
     P, M, V = params.copy(), np.zeros_like(params), np.zeros_like(params)
-    t0 = time.perf_counter()
-    for step in range(1, k + 1):
-        t = step - 1
-        orc.train_minibatch(d, hp, P, M, V, step, slots.obs[t], slots.actions[t], slots.adv[t], slots.ret[t],
+
+    def minibatch(c):
+        t = c % T
+        orc.train_minibatch(d, hp, P, M, V, c + 1, slots.obs[t], slots.actions[t], slots.adv[t], slots.ret[t],
                             slots.logp[t], threads=threads)
-    tm = (time.perf_counter() - t0) / k
+
+    k, dm = repeated(minibatch)
+    tm = dm / k
     it = tc + 4 * T * tm
     out["cpu_full_ppo_4096"] = {"env_steps_per_s": n * T / it, "cores": threads, "kind": "port",
-                                "sample": f"oracle collect of 4096 envs x 32 ({tc:.1f} s) and {k} minibatches of "
-                                          f"4096 rows ({tm:.2f} s each); iteration = collect + 128 minibatches"}
+                                "sample": f"oracle collect of 4096 envs x 32 ({nc} in {dc:.1f} s) and {k} minibatches "
+                                          f"of 4096 rows ({tm:.2f} s each); iteration = collect + 128 minibatches"}
     return out
 
 
