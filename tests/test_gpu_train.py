@@ -211,18 +211,20 @@ def test_full_loop_learns(mg):
     assert np.mean(lens[-3:]) > 1.5 * np.mean(lens[:3]), lens
 
 
-def test_full_size_iteration_properties(mg):
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_full_size_iteration_properties(mg, precision):
     """The BASELINE full-PPO configuration at full size (262144 envs, T = 32,
     4 epochs of 4096-row minibatches = 8192 Adam steps): every epoch visits each
     block once, every minibatch's LossStats are finite and in range, the weights
     stay finite, and a second model from the same seed reproduces the run bit
-    for bit (every reduction has a fixed order)."""
+    for bit (every reduction has a fixed order; in bf16 mode the weight
+    gradients come from the fused kernel)."""
     n, T, epochs = 262144, 32, 4
     blocks = T * n // 4096
 
     def run():
         gym = mg.Gym("rollout_cartpole", n, 0)
-        model = mg.PPOModel(gym, horizon=T)
+        model = mg.PPOModel(gym, horizon=T, precision=precision)
         model.collect()
         model.train(epochs)
         return model
