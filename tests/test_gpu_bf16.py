@@ -43,14 +43,17 @@ def test_bf16_forward_matches_oracle_and_differs_from_fp32(mg, orc, env):
     assert gap > 3 * err, (gap, err)
 
 
-@pytest.mark.parametrize("env,n,B,block,scale", [
-    ("cartpole", 2048, 512, 3, 4),
-    ("cartpole_continuous", 2048, 1024, 1, 4),
-    ("voxelnav16", 1024, 512, 2, 4),
-    ("cartpole", 4096, 4096, 1, 4),   # weight gradients: 8 row splits of 512 rows (two load batches)
-    ("cartpole", 6144, 6144, 0, 1),   # 16 splits of 384 rows (a partial load batch)
+@pytest.mark.parametrize("env,n,B,block,scale,layers", [
+    ("cartpole", 2048, 512, 3, 4, 2),
+    ("cartpole_continuous", 2048, 1024, 1, 4, 2),
+    ("voxelnav16", 1024, 512, 2, 4, 2),
+    ("cartpole", 4096, 4096, 1, 4, 2),   # fused weight gradients over 4096 rows
+    ("cartpole", 6144, 6144, 0, 1, 2),   # 64 tiles of 32x32: split kernel, 16 splits of 384 rows
+    ("cartpole", 1024, 512, 1, 8, 2),    # hidden 1024 (512 tiles, fused)
+    ("cartpole", 1024, 512, 1, 1, 8),    # 8 blocks (256 tiles, fused)
+    ("cartpole", 1024, 512, 0, 8, 8),    # the largest policy: 2048 tiles, split kernel
 ])
-def test_bf16_minibatch(mg, orc, env, n, B, block, scale):
+def test_bf16_minibatch(mg, orc, env, n, B, block, scale, layers):
     """One PPO minibatch in bf16 mode against the oracle's bf16 train step on
     the GPU's own rollout: recomputed head (median/p99/max), the Adam first
     moment (0.1 x the clipped gradient) per parameter group, post-Adam weights
@@ -61,8 +64,8 @@ def test_bf16_minibatch(mg, orc, env, n, B, block, scale):
     eid, kernel = ENVS[env]
     T = 2
     gym = mg.Gym(kernel, n, 0)
-    model = mg.PPOModel(gym, scale=scale, horizon=T, minibatch=B, precision="bf16")
-    d = orc.dims(eid, hidden=128 * scale, bf16=True)
+    model = mg.PPOModel(gym, scale=scale, layers=layers, horizon=T, minibatch=B, precision="bf16")
+    d = orc.dims(eid, hidden=128 * scale, layers=layers, bf16=True)
     model.collect()
     s = model.download_slots()
     p0 = model.params()
@@ -77,8 +80,8 @@ def test_bf16_minibatch(mg, orc, env, n, B, block, scale):
     assert max(errs.values()) < 1e-2, errs
     # the same gradient computed in fp32 is much further away
     P2, M2, V2 = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
-    orc.train_minibatch(orc.dims(eid, hidden=128 * scale), hp, P2, M2, V2, 1, *block_rows(s, n, B, block),
-                        threads=THREADS)
+    orc.train_minibatch(orc.dims(eid, hidden=128 * scale, layers=layers), hp, P2, M2, V2, 1,
+                        *block_rows(s, n, B, block), threads=THREADS)
     e32 = group_errors(model.pv, M2, M)
     assert e32["up0"] > 3 * errs["up0"], (e32["up0"], errs["up0"])
     assert_close(model.params(), P, TOL_TRAIN, "post-Adam weights")
