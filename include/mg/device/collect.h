@@ -58,6 +58,23 @@ struct LdsState {
                                     (size_t)163840 / CollectShape<M, O>::MIN_WG;
 };
 
+// LDS copies of the forward's small parameters for the T + 1 forwards of a
+// collect (W_in, b_in, every LN's gamma and beta, W_head): in LDS the embed,
+// LN and head phases, which no other workgroup's MFMAs overlap at one
+// workgroup per CU, read them without an L2 round trip. Used when they fit
+// beside the tile (and a staged State) at the kernel's workgroups per CU; else
+// the forward reads the arena.
+template <typename Env, int M, bool BF16>
+struct SmallStage {
+    static constexpr int O = Env::OBS_DIM, HD = Env::ACT_DIM + 1;
+    static constexpr int WIN = O * kEmbed, BIN = kEmbed, LN = (MG_MAX_LAYERS + 1) * 2 * kEmbed, WH = kEmbed * HD;
+    static constexpr int FLOATS = WIN + BIN + LN + WH;
+    using LS = LdsState<Env, M, BF16>;
+    static constexpr bool USE = sizeof(CollectSmem<M, O, HD, BF16>) + (LS::USE ? LS::BYTES : 0) +
+                                    (size_t)FLOATS * 4 <=
+                                (size_t)163840 / CollectShape<M, O>::MIN_WG;
+};
+
 // BF16: the policy forward multiplies bfloat16 operands (policy_bf16.h).
 template <typename Env, int M, bool BF16>
 __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectShape<M, Env::OBS_DIM>::MIN_WG))
@@ -71,6 +88,8 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
     __shared__ CollectSmem<M, O, HD, BF16> sm;
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
+    using SS = SmallStage<Env, M, BF16>;
+    __shared__ float small_lds[SS::USE ? SS::FLOATS : 1];
     FwdRegs<M, CS::W> R;
 
     const int tid = threadIdx.x;
@@ -103,6 +122,20 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     }
     float obs[O];
 
+    SmallParams sp = small_params(a.policy);
+    if constexpr (SS::USE) {  // ordered before the forwards by the barrier below
+        const mg_policy_view& pv = a.policy;
+        float* win = small_lds;
+        float* bin = win + SS::WIN;
+        float* ln = bin + SS::BIN;
+        float* wh = ln + SS::LN;
+        for (int k = tid; k < SS::WIN; k += CS::NT) win[k] = sp.win[k];
+        for (int k = tid; k < SS::BIN; k += CS::NT) bin[k] = sp.bin[k];
+        for (int k = tid; k < (int)(pv.layers + 1) * 2 * kEmbed; k += CS::NT) ln[k] = sp.ln[k];
+        for (int k = tid; k < SS::WH; k += CS::NT) wh[k] = sp.wh[k];
+        sp = {win, bin, ln, wh};
+    }
+
     if (envLane) {
         rng = a.rng[i];
         done = a.done[i];
@@ -129,9 +162,9 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
 
     for (uint32_t t = 0; t <= T; ++t) {
         if constexpr (BF16)
-            policy_forward_b<M, CS::W>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward_b<M, CS::W>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
         else
-            policy_forward<M, CS::W>(a.policy, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward<M, CS::W>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
         if (envLane) {
             const float* h = sm.head + tid * HD;
             if (t == T) {  // bootstrap head for GAE and headValue()

@@ -453,25 +453,42 @@ __device__ __forceinline__ void fwd_head(const float* Wh, Smem& sm, float* headL
     __syncthreads();
 }
 
+// Where a forward reads its small parameters: W_in [O][128], b_in, the LN
+// parameters (LN l: gamma at ln + 256 l, beta at ln + 256 l + 128; the arena
+// keeps them contiguous) and W_head [128][HD]; the arena itself, or copies in
+// LDS.
+struct SmallParams {
+    const float* win;
+    const float* bin;
+    const float* ln;
+    const float* wh;
+};
+__device__ __forceinline__ SmallParams small_params(const mg_policy_view& pv) {
+    return {pv.params + pv.off_in_w, pv.params + pv.off_in_b, pv.params + pv.off_ln_gamma[0],
+            pv.params + pv.off_head};
+}
+
 // Whole forward: obs staged in obsL ([M][O], LDS) -> head in headL ([M][HD], LDS).
 // 16-row tiles stream whole fragments (TStream), taller tiles half-fragments
 // (WStream).
 template <int M, int W = 4>
-__device__ __forceinline__ void policy_forward(const mg_policy_view& pv, FwdSmem<M>& sm, FwdRegs<M, W>& R,
-                                               const float* obsL, int O, float* headL, int HD) {
+__device__ __forceinline__ void policy_forward(const mg_policy_view& pv, const SmallParams& sp, FwdSmem<M>& sm,
+                                               FwdRegs<M, W>& R, const float* obsL, int O, float* headL, int HD) {
     using Stream = typename std::conditional<M == 16, TStream<M, W>, WStream<M, W>>::type;
     using Seq = FwdSeq<Shape<M, W>::MT>;
     const int NC = (int)pv.hidden / kChunk;
     const Seq seq{&pv, NC};
     Stream ws;
     ws.start(2 * (int)pv.layers * NC, seq);
-    fwd_embed<M, W>(pv.params + pv.off_in_w, pv.params + pv.off_in_b, obsL, O, R);
+    fwd_embed<M, W>(sp.win, sp.bin, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
-        fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l]);
+        const float* g = sp.ln + 2 * kEmbed * l;
+        fwd_layernorm<M, W>(sm, R, g, g + kEmbed);
         fwd_block<M, W, false, 1, Seq>(pv, (int)l, sm, R, ws, nullptr, seq);
     }
-    fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[pv.layers], pv.params + pv.off_ln_beta[pv.layers]);
-    fwd_head<M, W>(pv.params + pv.off_head, sm, headL, HD);
+    const float* g = sp.ln + 2 * kEmbed * pv.layers;
+    fwd_layernorm<M, W>(sm, R, g, g + kEmbed);
+    fwd_head<M, W>(sp.wh, sm, headL, HD);
 }
 
 }  // namespace dev

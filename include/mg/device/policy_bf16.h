@@ -254,22 +254,23 @@ __device__ __forceinline__ void fwd_block_b(const mg_policy_view& pv, int l, Fwd
 // Whole forward with bf16 GEMM operands: obs staged in obsL ([M][O], LDS) ->
 // head in headL ([M][HD], LDS).
 template <int M, int W = 4>
-__device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, FwdSmemB<M>& sm, FwdRegs<M, W>& R,
-                                                 const float* obsL, int O, float* headL, int HD) {
+__device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, const SmallParams& sp, FwdSmemB<M>& sm,
+                                                 FwdRegs<M, W>& R, const float* obsL, int O, float* headL, int HD) {
     using Stream = typename std::conditional<M == 16, TStreamB<M, W>, WStreamB<M, W>>::type;
     using Seq = FwdSeqB<Shape<M, W>::MT>;
     const int NC = (int)pv.hidden / kChunk;
     const Seq seq{&pv, NC};
     Stream ws;
     ws.start(2 * (int)pv.layers * NC, seq);
-    fwd_embed<M, W>(pv.params + pv.off_in_w, pv.params + pv.off_in_b, obsL, O, R);
+    fwd_embed<M, W>(sp.win, sp.bin, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
-        fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[l], pv.params + pv.off_ln_beta[l], nullptr, nullptr,
-                            nullptr, sm.xb);
+        const float* g = sp.ln + 2 * kEmbed * l;
+        fwd_layernorm<M, W>(sm, R, g, g + kEmbed, nullptr, nullptr, nullptr, sm.xb);
         fwd_block_b<M, W, false, 1, Seq>(pv, (int)l, sm, R, ws, nullptr, seq);
     }
-    fwd_layernorm<M, W>(sm, R, pv.params + pv.off_ln_gamma[pv.layers], pv.params + pv.off_ln_beta[pv.layers]);
-    fwd_head<M, W>(pv.params + pv.off_head, sm, headL, HD);
+    const float* g = sp.ln + 2 * kEmbed * pv.layers;
+    fwd_layernorm<M, W>(sm, R, g, g + kEmbed);
+    fwd_head<M, W>(sp.wh, sm, headL, HD);
 }
 
 }  // namespace dev

@@ -28,9 +28,9 @@ __global__ void __launch_bounds__(256) forward_kernel(const mg_policy_view pv, c
     }
     __syncthreads();
     if constexpr (BF16)
-        policy_forward_b<M>(pv, sm, R, obsL, O, headL, HD);
+        policy_forward_b<M>(pv, small_params(pv), sm, R, obsL, O, headL, HD);
     else
-        policy_forward<M>(pv, sm, R, obsL, O, headL, HD);
+        policy_forward<M>(pv, small_params(pv), sm, R, obsL, O, headL, HD);
     for (int idx = threadIdx.x; idx < M * HD; idx += 256) {
         const uint32_t r = row0 + idx / HD;
         if (r < rows) head[(size_t)row0 * HD + idx] = headL[idx];
