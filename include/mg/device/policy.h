@@ -441,8 +441,12 @@ __device__ __forceinline__ void fwd_head(const float* Wh, Smem& sm, float* headL
     const float* wp = Wh + c0 * HD;
     const float* xr = sm.xs + row * kLds + c0;
     float x[CPT];
+    static_assert(CPT % 4 == 0, "float4 columns");
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) x[c] = xr[c];
+    for (int c = 0; c < CPT; c += 4) {  // float4 reads: no bank conflicts between lanes
+        const f32x4 v = *reinterpret_cast<const f32x4*>(xr + c);
+        x[c] = v[0], x[c + 1] = v[1], x[c + 2] = v[2], x[c + 3] = v[3];
+    }
     for (int j = 0; j < HD; ++j) {
         float acc = 0.0f;
 #pragma unroll

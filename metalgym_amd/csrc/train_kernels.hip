@@ -125,22 +125,29 @@ __device__ __forceinline__ void bwd_layernorm(Smem& sm, TRegs& G, const float* x
     tile_colsum2<kTR>(sm.xs, xn, tp_beta, tp_gamma);  // reads the tile before the in-place update below
     __syncthreads();
     const int row = tid / TPR, part = tid % TPR, c0 = part * CPT;
-    float* zr = sm.xs + row * kLds + c0;
-    const float* xr = xn + row * kEmbed + c0;
-    float dxn[CPT], xv[CPT];
+    static_assert(CPT == 4, "one float4 per thread");
+    // float4 accesses: a thread's 4 columns are 16 contiguous bytes, so the
+    // lanes of a wave touch distinct banks (scalar accesses at a 4-dword
+    // lane stride would conflict 4 ways)
+    f32x4* zr = reinterpret_cast<f32x4*>(sm.xs + row * kLds + c0);
+    const f32x4 xv = *reinterpret_cast<const f32x4*>(xn + row * kEmbed + c0);
+    const f32x4 gm = *reinterpret_cast<const f32x4*>(gamma + c0);
+    const f32x4 z = *zr;
+    float dxn[CPT];
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        xv[c] = xr[c];
-        dxn[c] = zr[c] * gamma[c0 + c];
+        dxn[c] = z[c] * gm[c];
         s1 += dxn[c];
         s2 += dxn[c] * xv[c];
     }
     s1 = group_sum<TPR>(s1);
     s2 = group_sum<TPR>(s2);
     const float r1 = s1 / (float)kEmbed, r2 = s2 / (float)kEmbed, rd = 1.0f / sd[row];
+    f32x4 o;
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) zr[c] = rd * (dxn[c] - r1 - xv[c] * r2);
+    for (int c = 0; c < CPT; ++c) o[c] = rd * (dxn[c] - r1 - xv[c] * r2);
+    *zr = o;
     __syncthreads();
     for_each_elem<kTR, kTW>(
         [&](int rt, int ct, int r, int row2, int col) { G.h[rt][ct][r] = sm.xs[row2 * kLds + col]; });
