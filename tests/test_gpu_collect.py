@@ -56,6 +56,7 @@ def run_collect_parity(mg, orc, env, n, T, layers=2, scale=4, seed=0, collects=2
     ("cartpole", 4096, 8),
     ("cartpole", 64 * 576, 2),   # 64-row tiles (n >= 64 * 512)
     ("cartpole_continuous", 2048, 8),
+    ("cartpole_continuous_clamp", 2048, 8),
     ("voxelnav16", 1024, 8),
     ("voxelnav", 1024, 8),       # heightmaps staged in LDS: 16-row tiles
     ("voxelnav", 8192, 2),       # 32-row tiles

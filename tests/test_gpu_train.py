@@ -124,6 +124,7 @@ def float64_moment(pv, params, rows, hp):
     ("cartpole", 2048, 2, 512, 5, 2, 4),
     ("cartpole", 1280, 2, 320, 3, 2, 4),      # minibatch not a multiple of 128
     ("cartpole_continuous", 2048, 2, 1024, 2, 2, 4),
+    ("cartpole_continuous_clamp", 2048, 2, 1024, 0, 2, 4),
     ("voxelnav16", 1024, 2, 512, 1, 2, 4),
     ("voxelnav", 1024, 2, 512, 1, 2, 4),
     ("cartpole", 1024, 2, 512, 2, 3, 2),      # hidden 256, three blocks
@@ -151,7 +152,7 @@ def test_one_minibatch(mg, orc, env, n, T, B, block, layers, scale):
     assert np.all(np.isfinite(p1))
 
 
-@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous"])
+@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "cartpole_continuous_clamp", "voxelnav"])
 def test_train_epochs(mg, orc, env):
     """train(2) over 2 slots x 2 blocks: the block order and every minibatch's
     LossStats match the oracle's train loop; weights stay within 1e-3."""
