@@ -101,3 +101,44 @@ def test_bf16_full_loop_learns(mg):
         model.train(4)
         assert np.all(np.isfinite(model.last_stats().as_tuple()))
     assert np.mean(lens[-3:]) > 1.5 * np.mean(lens[:3]), lens
+
+
+@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous"])
+def test_bf16_train_epochs(mg, orc, env):
+    """train(2) in bf16 mode over 2 slots x 2 blocks against the oracle's bf16
+    train loop: the same block order, every minibatch's LossStats and the
+    weights after 2 epochs within 1e-3. The clip fraction counts rows with
+    |ratio - 1| > clip; bf16 rounding flips move about 1% of head values by
+    more than 1e-5, so up to 1% of the rows (at least 2) may sit on the other
+    side of the clip boundary."""
+    import ctypes as C
+
+    from parity import TOL_TRAIN, assert_close
+
+    n, T, B = 1024, 2, 512
+    eid, kernel = ENVS[env]
+    gym = mg.Gym(kernel, n, 7)
+    model = mg.PPOModel(gym, horizon=T, seed=7, minibatch=B, precision="bf16")
+    d = orc.dims(eid, bf16=True)
+    model.collect()
+    s = model.download_slots()
+    p0 = model.params()
+    model.train(2)
+    stats = model.train_stats()
+    P, M, V = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    step, shuf = C.c_uint32(0), C.c_uint64(0)
+    orc.lib().orc_shuffle_state_init(7, C.byref(shuf))
+    blocks = T * (n // B)
+    order = np.arange(blocks, dtype=np.uint32)
+    ost = (orc.Stats * (2 * blocks))()
+    orc.lib().orc_train(C.byref(d), C.byref(orc.hparams()), orc.ptr(P), orc.ptr(M), orc.ptr(V), C.byref(step),
+                        C.byref(shuf), n, T, B, 2, orc.ptr(np.ascontiguousarray(s["obs"])),
+                        orc.ptr(np.ascontiguousarray(s["actions"])), orc.ptr(np.ascontiguousarray(s["adv"])),
+                        orc.ptr(np.ascontiguousarray(s["ret"])), orc.ptr(np.ascontiguousarray(s["logp"])), ost,
+                        orc.ptr(order), THREADS)
+    assert list(model.last_order()[-blocks:]) == list(order)
+    ostats = np.array([ost[i].as_tuple() for i in range(2 * blocks)], np.float32)
+    cols = [0, 1, 2, 3, 5]
+    assert_close(stats[:, cols], ostats[:, cols], TOL_TRAIN, "per-minibatch LossStats")
+    assert np.all(np.abs(stats[:, 4] - ostats[:, 4]) * B <= max(2, B // 100) + 1e-3), (stats[:, 4], ostats[:, 4])
+    assert_close(model.params(), P, TOL_TRAIN, "weights after 2 epochs")
