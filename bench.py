@@ -1,7 +1,7 @@
 """Benchmark of the rollout-and-policy hot path on one MI355X.
 
 Headline: CartPole with policy, collect() at 262144 envs, T = 32, the 2-block
-residual MLP (embed 128, hidden 512) -- BASELINE.json config 2 at its largest
+residual MLP (embed 128, hidden 512) -- the reference's collect benchmark at its largest
 size. One step = one collect() (262144 x 32 env steps, policy forward on fp32
 MFMA, sampling, env step, GAE). Inputs are synthetic (seeded envs and weights)
 and resident on the GPU. The other configurations (random policy, full PPO loop,
@@ -165,7 +165,7 @@ def cpu_baseline(target_s=10.0):
 
 
 def cpu_extras(threads=None):
-    """The oracle on the host for the other BASELINE configurations, bounded:
+    """The oracle on the host for the other benchmark configurations, bounded:
     the random rollout at 262144 envs (config 1), and the full PPO loop at 4096
     envs (config 3) from one collect and a few timed minibatches, an iteration
     being one collect plus 4 epochs x 32 minibatches of 4096 rows."""

@@ -88,7 +88,7 @@ void cp_step(CPState& s, float force, float* obs, float& reward, uint8_t& done) 
     done = (terminated || truncated) ? 1 : 0;
 }
 
-// ---- VoxelNav16: BASELINE config 5 specification (no reference code) -----
+// ---- VoxelNav16: navigation in a 16^3 voxel grid (no reference code) -----
 const int kG = 16;
 const int kCells = kG * kG * kG;
 struct VNState {
@@ -335,7 +335,7 @@ void env_step(int env, void* state, const void* action, float* obs, float& rewar
             cp_step(*static_cast<CPState*>(state), a == 1 ? kForceMag : -kForceMag, obs, reward, done);
             break;
         }
-        case ORC_CARTPOLE_CONT: {  // BASELINE: force = 10 tanh(a)
+        case ORC_CARTPOLE_CONT: {  // force = 10 tanh(a)
             float a;
             std::memcpy(&a, action, 4);
             cp_step(*static_cast<CPState*>(state), kForceMag * mg::tanhf(a), obs, reward, done);

@@ -1,4 +1,4 @@
-"""Shared helpers of the GPU parity tests (tolerances from BASELINE.json's north_star)."""
+"""Shared helpers of the GPU parity tests: the tolerances of each compared quantity."""
 import os
 
 import numpy as np

@@ -313,7 +313,7 @@ def test_shuffle_is_a_seeded_permutation(orc):
     assert sorted(c) == list(range(64)) and not np.array_equal(c, a)
 
 
-# ---- VoxelNav16 (BASELINE config 5 specification) -------------------------------------
+# ---- VoxelNav16 (navigation in a 16^3 voxel grid) -------------------------------------
 
 def vn_fields(state):
     head = state[:32].view(np.int32)

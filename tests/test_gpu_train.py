@@ -214,7 +214,7 @@ def test_full_loop_learns(mg):
 
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
 def test_full_size_iteration_properties(mg, precision):
-    """The BASELINE full-PPO configuration at full size (262144 envs, T = 32,
+    """The benchmarked full-PPO configuration at full size (262144 envs, T = 32,
     4 epochs of 4096-row minibatches = 8192 Adam steps): every epoch visits each
     block once, every minibatch's LossStats are finite and in range, the weights
     stay finite, and a second model from the same seed reproduces the run bit
