@@ -131,6 +131,7 @@ def float64_moment(pv, params, rows, hp):
     ("cartpole", 1024, 2, 512, 1, 5, 2),      # five blocks
     ("cartpole", 1024, 2, 512, 0, 8, 1),      # the most blocks (MG_MAX_LAYERS), hidden 128
     ("cartpole", 1024, 2, 512, 1, 2, 8),      # the widest hidden layer (scale 8: 1024)
+    ("cartpole", 1024, 2, 512, 1, 1, 2),      # one block, hidden 256
 ])
 def test_one_minibatch(mg, orc, env, n, T, B, block, layers, scale):
     gym, model, d = setup(mg, orc, env, n, T, B, layers=layers, scale=scale)
