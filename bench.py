@@ -228,7 +228,8 @@ def pmc_traffic():
 def profile_pass(which):
     """Short runs of each kernel for rocprofv3 (--kernel-trace / --pmc): the
     262144-env collect and random rollout, 64 train minibatches, and one 1 GiB
-    device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters.
+    device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters
+    ("all" adds 64 copies of the Adam step's byte count, its size floor).
     "bf16": the collect and the minibatches in bf16 mode, and the copy."""
     import metalgym_amd as mg
 
@@ -261,6 +262,16 @@ def profile_pass(which):
         mg.lib().mg_memcpy_d2d(b.ptr, a.ptr, nbytes)
         sync()
         print(f"profile: one device copy of {nbytes} bytes", flush=True)
+        if which == "all":
+            # the floor of a kernel of the Adam step's size: copies that move its
+            # 28 B per parameter (14 B read + 14 B written), each from and to a
+            # region no earlier copy touched (not in L2)
+            gym = mg.Gym("rollout_cartpole", 4096, 0)
+            small = mg.PPOModel(gym, horizon=T).pv.count * 14
+            for k in range(64):
+                mg.lib().mg_memcpy_d2d(b.ptr + k * small, a.ptr + k * small, small)
+            sync()
+            print(f"profile: 64 device copies of {small} bytes", flush=True)
 
 
 def main():

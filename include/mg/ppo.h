@@ -7,6 +7,7 @@
 // accessors return host mirrors that are refreshed lazily after each collect()
 // or train(); their pointers stay valid until the model is destroyed.
 #pragma once
+#include <algorithm>
 #include <cmath>
 #include <random>
 #include <type_traits>
