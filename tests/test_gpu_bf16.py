@@ -45,6 +45,7 @@ def test_bf16_forward_matches_oracle_and_differs_from_fp32(mg, orc, env):
 
 @pytest.mark.parametrize("env,n,B,block,scale,layers", [
     ("cartpole", 2048, 512, 3, 4, 2),
+    ("cartpole", 64, 64, 1, 4, 2),       # the smallest minibatch: split kernel, one split
     ("cartpole_continuous", 2048, 1024, 1, 4, 2),
     ("voxelnav16", 1024, 512, 2, 4, 2),
     ("cartpole", 4096, 4096, 1, 4, 2),   # fused weight gradients over 4096 rows

@@ -54,6 +54,8 @@ def run_collect_parity(mg, orc, env, n, T, layers=2, scale=4, seed=0, collects=2
 
 @pytest.mark.parametrize("env,n,T", [
     ("cartpole", 4096, 8),
+    ("cartpole", 64, 1),         # the fewest envs (four 16-row tiles), one step
+    ("cartpole", 192, 3),
     ("cartpole", 64 * 576, 2),   # 64-row tiles (n >= 64 * 512)
     ("cartpole_continuous", 2048, 8),
     ("cartpole_continuous_clamp", 2048, 8),

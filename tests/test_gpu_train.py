@@ -123,6 +123,7 @@ def float64_moment(pv, params, rows, hp):
     ("cartpole", 4096, 2, 4096, 1, 2, 4),
     ("cartpole", 2048, 2, 512, 5, 2, 4),
     ("cartpole", 1280, 2, 320, 3, 2, 4),      # minibatch not a multiple of 128
+    ("cartpole", 64, 2, 64, 1, 2, 4),         # the smallest minibatch and env count
     ("cartpole_continuous", 2048, 2, 1024, 2, 2, 4),
     ("cartpole_continuous_clamp", 2048, 2, 1024, 0, 2, 4),
     ("voxelnav16", 1024, 2, 512, 1, 2, 4),
