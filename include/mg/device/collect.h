@@ -59,20 +59,26 @@ struct LdsState {
 };
 
 // LDS copies of the forward's small parameters for the T + 1 forwards of a
-// collect (W_in, b_in, every LN's gamma and beta, W_head): in LDS the embed,
-// LN and head phases, which no other workgroup's MFMAs overlap at one
-// workgroup per CU, read them without an L2 round trip. Used when they fit
-// beside the tile (and a staged State) at the kernel's workgroups per CU; else
-// the forward reads the arena.
+// collect (W_in, b_in, the layers + 1 LNs' gamma and beta, W_head), in the
+// kernel's dynamic LDS: the embed, LN and head phases then read them without
+// an L2 round trip (at one workgroup per CU no other workgroup's MFMAs overlap
+// that latency; at two, 64-row tiles, it took the 262144-env CartPole collect
+// from 36.0 to 34.9 ms). Used when they fit beside the tile (and a staged
+// State) at the kernel's workgroups per CU; else the forward reads the arena.
+// Host and kernel evaluate the same predicate: the launch passes floats() * 4
+// bytes of dynamic LDS exactly when fits() holds.
 template <typename Env, int M, bool BF16>
 struct SmallStage {
     static constexpr int O = Env::OBS_DIM, HD = Env::ACT_DIM + 1;
-    static constexpr int WIN = O * kEmbed, BIN = kEmbed, LN = (MG_MAX_LAYERS + 1) * 2 * kEmbed, WH = kEmbed * HD;
-    static constexpr int FLOATS = WIN + BIN + LN + WH;
+    static constexpr int WIN = O * kEmbed, BIN = kEmbed, WH = kEmbed * HD;
     using LS = LdsState<Env, M, BF16>;
-    static constexpr bool USE = sizeof(CollectSmem<M, O, HD, BF16>) + (LS::USE ? LS::BYTES : 0) +
-                                    (size_t)FLOATS * 4 <=
-                                (size_t)163840 / CollectShape<M, O>::MIN_WG;
+    static constexpr size_t STATIC = sizeof(CollectSmem<M, O, HD, BF16>) + (LS::USE ? LS::BYTES : 0);
+    __host__ __device__ static constexpr uint32_t floats(uint32_t layers) {
+        return WIN + BIN + (layers + 1) * 2 * kEmbed + WH;
+    }
+    __host__ __device__ static constexpr bool fits(uint32_t layers) {
+        return STATIC + (size_t)floats(layers) * 4 <= (size_t)163840 / CollectShape<M, O>::MIN_WG;
+    }
 };
 
 // BF16: the policy forward multiplies bfloat16 operands (policy_bf16.h).
@@ -89,7 +95,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     __shared__ CollectSmem<M, O, HD, BF16> sm;
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     using SS = SmallStage<Env, M, BF16>;
-    __shared__ float small_lds[SS::USE ? SS::FLOATS : 1];
+    extern __shared__ float small_lds[];  // SS::floats(layers) floats when SS::fits(layers)
     FwdRegs<M, CS::W> R;
 
     const int tid = threadIdx.x;
@@ -123,15 +129,17 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     float obs[O];
 
     SmallParams sp = small_params(a.policy);
-    if constexpr (SS::USE) {  // ordered before the forwards by the barrier below
-        const mg_policy_view& pv = a.policy;
+    // a runtime choice: a template parameter instead (LDS instructions for the
+    // small parameters) measured slower at 4096 and 262144 envs, fp32 and bf16
+    if (SS::fits(a.policy.layers)) {  // ordered before the forwards by the barrier below
+        const int lnf = (int)(a.policy.layers + 1) * 2 * kEmbed;
         float* win = small_lds;
         float* bin = win + SS::WIN;
         float* ln = bin + SS::BIN;
-        float* wh = ln + SS::LN;
+        float* wh = ln + lnf;
         for (int k = tid; k < SS::WIN; k += CS::NT) win[k] = sp.win[k];
         for (int k = tid; k < SS::BIN; k += CS::NT) bin[k] = sp.bin[k];
-        for (int k = tid; k < (int)(pv.layers + 1) * 2 * kEmbed; k += CS::NT) ln[k] = sp.ln[k];
+        for (int k = tid; k < lnf; k += CS::NT) ln[k] = sp.ln[k];
         for (int k = tid; k < SS::WH; k += CS::NT) wh[k] = sp.wh[k];
         sp = {win, bin, ln, wh};
     }
@@ -208,22 +216,26 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     }
 }
 
+template <typename Env, int M, bool BF16>
+void launch_collect_m(const mg_collect_args* a, hipStream_t st) {
+    using SS = SmallStage<Env, M, BF16>;
+    const uint32_t L = a->policy.layers;
+    const dim3 grid(a->n / M), block(CollectShape<M, Env::OBS_DIM>::NT);
+    hipLaunchKernelGGL((collect_kernel<Env, M, BF16>), grid, block, SS::fits(L) ? SS::floats(L) * 4 : 0, st, *a);
+}
+
 template <typename Env, bool BF16>
 int launch_collect_tiles(const mg_collect_args* a) {
     hipStream_t st = static_cast<hipStream_t>(a->stream);
     // 64-row tiles reuse each weight fragment across the most rows; they need
     // n / 64 >= 512 workgroups (2 per CU) to fill the chip. Smaller runs use
     // 32-row, then 16-row tiles for more workgroups.
-    if (a->n >= 64u * 512u) {
-        hipLaunchKernelGGL((collect_kernel<Env, 64, BF16>), dim3(a->n / 64), dim3(CollectShape<64, Env::OBS_DIM>::NT),
-                           0, st, *a);
-    } else if (a->n >= 32u * 256u) {
-        hipLaunchKernelGGL((collect_kernel<Env, 32, BF16>), dim3(a->n / 32), dim3(CollectShape<32, Env::OBS_DIM>::NT),
-                           0, st, *a);
-    } else {
-        hipLaunchKernelGGL((collect_kernel<Env, 16, BF16>), dim3(a->n / 16), dim3(CollectShape<16, Env::OBS_DIM>::NT),
-                           0, st, *a);
-    }
+    if (a->n >= 64u * 512u)
+        launch_collect_m<Env, 64, BF16>(a, st);
+    else if (a->n >= 32u * 256u)
+        launch_collect_m<Env, 32, BF16>(a, st);
+    else
+        launch_collect_m<Env, 16, BF16>(a, st);
     return (int)hipGetLastError();
 }
 
