@@ -221,7 +221,8 @@ struct WStream {
         // raised wave priority while issuing MFMAs: the other workgroup on the
         // CU is then in its LN / head / env phase, whose VALU and LDS work
         // fills the gaps instead of delaying the MFMA issue (0.6% on the
-        // 262144-env collect)
+        // 262144-env collect while the small parameters came from L2; no
+        // measurable difference since they are staged in LDS)
         __builtin_amdgcn_s_setprio(1);
         gemm_frag<M, W, NG>(acc, a_lds, b[0], 0);
         if (more) load_frag<M, W, NG>(b[0], f, 0);
