@@ -115,7 +115,7 @@ def test_collect_full_size_subset(mg, orc):
     (1024, 2, 8, 1),     # the most blocks (MG_MAX_LAYERS), 16-row tiles
     (1024, 2, 2, 8),     # the widest hidden layer (1024), 16-row tiles
     (8192, 2, 2, 8),     # 32-row tiles
-    (32768, 2, 8, 1),    # 64-row tiles
+    (32768, 2, 8, 1),    # 64-row tiles; 9 LNs: small parameters read from the arena, not LDS
 ])
 def test_collect_other_shapes(mg, orc, n, T, layers, scale):
     run_collect_parity(mg, orc, "cartpole", n, T, layers=layers, scale=scale, seed=11, collects=1)
