@@ -68,47 +68,60 @@ def build() -> None:
 _lib = None
 
 
+def _signatures():
+    P = C.c_void_p
+    u32, f32 = C.c_uint32, C.c_float
+    return {
+        "orc_rng_next": (u32, [P]),
+        "orc_rng_uniform": (f32, [P]),
+        "orc_rng_uniform_range": (f32, [P, f32, f32]),
+        "orc_rng_int": (u32, [P, u32]),
+        "orc_gym_init": (None, [C.c_int, u32, u32, P, P, P, P]),
+        "orc_env_info_get": (C.c_int, [C.c_int, P]),
+        "orc_env_reset": (None, [C.c_int, P, P]),
+        "orc_env_step": (None, [C.c_int, P, P, P, P, P]),
+        "orc_rollout": (None, [C.c_int, u32, u32, C.c_int, P, P, P, P, P, P, P, P, C.c_int]),
+        "orc_round_bf16": (f32, [f32]),
+        "orc_expf": (f32, [f32]),
+        "orc_logf": (f32, [f32]),
+        "orc_sinf": (f32, [f32]),
+        "orc_cosf": (f32, [f32]),
+        "orc_tanhf": (f32, [f32]),
+        "orc_layout_get": (C.c_int, [P, P]),
+        "orc_init_params": (None, [P, u32, P]),
+        "orc_splitmix_next": (C.c_uint64, [P]),
+        "orc_forward": (None, [P, P, P, u32, P, C.c_int]),
+        "orc_sample": (None, [P, P, P, u32, P, P, P, P]),
+        "orc_gae": (None, [P, P, P, P, u32, u32, u32, u32, f32, f32, P, P]),
+        "orc_collect": (None, [C.c_int, P, P, u32, u32, C.c_int, f32, f32] + [P] * 14 + [C.c_int]),
+        "orc_train_minibatch": (None, [P, P, P, P, P, u32, u32, P, P, P, P, P, P, P, P, C.c_int]),
+        "orc_train_minibatch_masked": (None, [P, P, P, P, P, u32, u32, P, P, P, P, P, P, P, P, P, P, C.c_int]),
+        "orc_shuffle_state_init": (None, [u32, P]),
+        "orc_shuffle_blocks": (None, [P, P, u32]),
+        "orc_train": (None, [P, P, P, P, P, P, P, u32, u32, u32, u32, P, P, P, P, P, P, P, C.c_int]),
+    }
+
+
+def load(path: str):
+    """Load an oracle build and declare its signatures."""
+    L = C.CDLL(path)
+    for name, (res, args) in _signatures().items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
 def lib():
+    """The oracle library. MG_ORACLE_LIB names another build of oracle.cpp
+    (the mutation tests load deliberately broken copies this way); by default
+    the in-tree build, made on first use."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
+        path = os.environ.get("MG_ORACLE_LIB") or LIB_PATH
+        if path == LIB_PATH and not os.path.exists(LIB_PATH):
             build()
-        L = C.CDLL(LIB_PATH)
-        P = C.c_void_p
-        u32, f32 = C.c_uint32, C.c_float
-        sig = {
-            "orc_rng_next": (u32, [P]),
-            "orc_rng_uniform": (f32, [P]),
-            "orc_rng_uniform_range": (f32, [P, f32, f32]),
-            "orc_rng_int": (u32, [P, u32]),
-            "orc_gym_init": (None, [C.c_int, u32, u32, P, P, P, P]),
-            "orc_env_info_get": (C.c_int, [C.c_int, P]),
-            "orc_env_reset": (None, [C.c_int, P, P]),
-            "orc_env_step": (None, [C.c_int, P, P, P, P, P]),
-            "orc_rollout": (None, [C.c_int, u32, u32, C.c_int, P, P, P, P, P, P, P, P, C.c_int]),
-            "orc_round_bf16": (f32, [f32]),
-            "orc_expf": (f32, [f32]),
-            "orc_logf": (f32, [f32]),
-            "orc_sinf": (f32, [f32]),
-            "orc_cosf": (f32, [f32]),
-            "orc_tanhf": (f32, [f32]),
-            "orc_layout_get": (C.c_int, [P, P]),
-            "orc_init_params": (None, [P, u32, P]),
-            "orc_splitmix_next": (C.c_uint64, [P]),
-            "orc_forward": (None, [P, P, P, u32, P, C.c_int]),
-            "orc_sample": (None, [P, P, P, u32, P, P, P, P]),
-            "orc_gae": (None, [P, P, P, P, u32, u32, u32, u32, f32, f32, P, P]),
-            "orc_collect": (None, [C.c_int, P, P, u32, u32, C.c_int, f32, f32] + [P] * 14 + [C.c_int]),
-            "orc_train_minibatch": (None, [P, P, P, P, P, u32, u32, P, P, P, P, P, P, P, P, C.c_int]),
-            "orc_shuffle_state_init": (None, [u32, P]),
-            "orc_shuffle_blocks": (None, [P, P, u32]),
-            "orc_train": (None, [P, P, P, P, P, P, P, u32, u32, u32, u32, P, P, P, P, P, P, P, C.c_int]),
-        }
-        for name, (res, args) in sig.items():
-            fn = getattr(L, name)
-            fn.restype = res
-            fn.argtypes = args
-        _lib = L
+        _lib = load(path)
     return _lib
 
 
@@ -245,3 +258,25 @@ def train_minibatch(d: Dims, hp: HParams, params, m, v, step, obs, actions, adv,
                               ptr(np.ascontiguousarray(old_logp, np.float32)), ptr(grad), C.byref(st), ptr(head),
                               threads)
     return st, grad, head
+
+
+def train_minibatch_masked(d: Dims, hp: HParams, params, m, v, step, obs, actions, adv, ret, old_logp, relu_mask,
+                           threads: int = 8):
+    """train_minibatch with the forward's ReLU decisions given (relu_mask
+    [rows][layers][hidden], bool or uint8; None keeps z > 0); returns (stats,
+    grad, head, preact) with the pre-activations [rows][layers][hidden]."""
+    rows = obs.shape[0]
+    grad = np.zeros_like(params)
+    head = np.zeros((rows, d.act_dim + 1), np.float32)
+    preact = np.zeros((rows, d.layers, d.hidden), np.float32)
+    mask = None if relu_mask is None else np.ascontiguousarray(relu_mask, np.uint8)
+    if mask is not None:
+        assert mask.shape == preact.shape, (mask.shape, preact.shape)
+    st = Stats()
+    lib().orc_train_minibatch_masked(C.byref(d), C.byref(hp), ptr(params), ptr(m), ptr(v), step, rows,
+                                     ptr(np.ascontiguousarray(obs, np.float32)), ptr(np.ascontiguousarray(actions)),
+                                     ptr(np.ascontiguousarray(adv, np.float32)),
+                                     ptr(np.ascontiguousarray(ret, np.float32)),
+                                     ptr(np.ascontiguousarray(old_logp, np.float32)), ptr(grad), C.byref(st),
+                                     ptr(head), ptr(mask), ptr(preact), threads)
+    return st, grad, head, preact
