@@ -3,6 +3,7 @@
 // checked for the invariants the reference documents (README.md:100-156).
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <random>
 
 #include "mg/envs/cartpole.h"
@@ -20,6 +21,42 @@ static int failures = 0;
 
 int main() {
     const uint32_t N = 256, T = 8;
+    {  // Gym::stepInto (gym.h:94-108) into slot t of device buffers gives the same
+        // steps as Gym::run with the same actions
+        const uint32_t S = 40;
+        Gym<CartPole> a(N), b(N);
+        std::vector<int> acts((size_t)S * N);
+        std::mt19937 gen(5);
+        for (auto& x : acts) x = (int)(gen() & 1u);
+        void *dAct = nullptr, *dObs = nullptr, *dRew = nullptr;
+        CHECK(mg_malloc(&dAct, acts.size() * sizeof(int)) == MG_OK);
+        CHECK(mg_malloc(&dObs, acts.size() * sizeof(CartPole::Obs)) == MG_OK);
+        CHECK(mg_malloc(&dRew, acts.size() * sizeof(float)) == MG_OK);
+        CHECK(mg_memcpy_h2d(dAct, acts.data(), acts.size() * sizeof(int)) == MG_OK);
+        for (uint32_t t = 0; t < S; t++)
+            a.stepInto(static_cast<const int*>(dAct) + (size_t)t * N, static_cast<CartPole::Obs*>(dObs) + (size_t)t * N,
+                       static_cast<float*>(dRew) + (size_t)t * N);
+        CHECK(mg_gym_sync(a.handle) == MG_OK);
+        std::vector<CartPole::Obs> obs(acts.size());
+        std::vector<float> rew(acts.size());
+        CHECK(mg_memcpy_d2h(obs.data(), dObs, obs.size() * sizeof(CartPole::Obs)) == MG_OK);
+        CHECK(mg_memcpy_d2h(rew.data(), dRew, rew.size() * sizeof(float)) == MG_OK);
+        std::vector<float> r(N);
+        uint32_t ended = 0;
+        for (uint32_t t = 0; t < S; t++) {
+            for (uint32_t i = 0; i < N; i++) b.actions()[i] = acts[(size_t)t * N + i];
+            b.run(r);
+            CHECK(std::memcmp(b.obs(), &obs[(size_t)t * N], N * sizeof(CartPole::Obs)) == 0);
+            CHECK(std::memcmp(r.data(), &rew[(size_t)t * N], N * sizeof(float)) == 0);
+            const uint8_t* db = b.done();
+            for (uint32_t i = 0; i < N; i++) ended += db[i];
+        }
+        CHECK(std::memcmp(a.done(), b.done(), N) == 0);
+        CHECK(ended > 0);  // resets happened between the steps
+        mg_free(dAct);
+        mg_free(dObs);
+        mg_free(dRew);
+    }
     {
         Gym<CartPole> gym(N);
         const uint8_t* d0 = gym.done();

@@ -327,6 +327,19 @@ int mg_ppo_set_params(mg_ppo* model, const float* host, uint32_t count);
 /* Re-derives the fragment-tiled copies after the caller wrote params through
  * the device view. */
 int mg_ppo_params_updated(mg_ppo* model);
+/* Activation captures of the last train minibatch (the row pass writes them
+ * for the weight gradients), for tests and debugging; no reference
+ * counterpart (the reference keeps its activations in internal buffers,
+ * model/ppo.h:355-372). which = MG_CAPTURE_*: the LN outputs entering each
+ * block ([layers][B][128]), the relu'd hidden activations ([layers][B][hidden]),
+ * the gradients at the block outputs ([layers][B][128]) and the masked hidden
+ * gradients ([layers][B][hidden]). MG_PRECISION_FP32: fp32, row-major.
+ * MG_PRECISION_BF16: bfloat16 bit patterns, row-group-packed (element (r, c)
+ * of a C-column capture at ((r / 8) C + c) 8 + r % 8). *ptr is a device
+ * pointer valid until the next train call; MG_ERR_STATE before the first. */
+enum { MG_CAPTURE_LN_OUT = 0, MG_CAPTURE_HIDDEN = 1, MG_CAPTURE_DH = 2, MG_CAPTURE_DV = 3 };
+int mg_ppo_train_capture(mg_ppo* model, uint32_t which, const void** ptr, uint32_t* rows, uint32_t* cols,
+                         uint32_t* layers);
 /* Adam state: first and second moments, same layout as the parameters. */
 int mg_ppo_adam_state(mg_ppo* model, float** m, float** v, uint32_t* step);
 /* model/ppo.h:460-469 (Gaussian head only). */

@@ -139,6 +139,7 @@ def lib():
         "mg_ppo_set_params": (I, [P, P, u32]),
         "mg_ppo_params_updated": (I, [P]),
         "mg_ppo_adam_state": (I, [P, P, P, P]),
+        "mg_ppo_train_capture": (I, [P, u32, P, P, P, P]),
         "mg_ppo_set_log_std": (I, [P, f32]),
         "mg_ppo_last_order": (I, [P, P, u32, P]),
         "mg_ppo_sample": (I, [P, P, u32, P, P, P, P]),
@@ -302,6 +303,11 @@ class Gym:
         check(lib().mg_gym_run(self.h))
         self.sync()
 
+    def step_into(self, actions_ptr: int, obs_ptr: int, reward_ptr: int) -> None:
+        """gym.h:94-108 (encodeStep): one step reading device actions and writing
+        device obs and rewards at the given addresses. Asynchronous."""
+        check(lib().mg_gym_step_into(self.h, actions_ptr, obs_ptr, reward_ptr))
+
     def _slot_bufs(self, steps):
         n = self.n
         acts = DeviceBuffer(steps * n * self.action_bytes)
@@ -425,6 +431,18 @@ class PPOModel:
         m, v, st = C.c_void_p(), C.c_void_p(), u32()
         check(lib().mg_ppo_adam_state(self.h, C.byref(m), C.byref(v), C.byref(st)))
         return d2h(m.value, np.float32, (self.pv.count,)), d2h(v.value, np.float32, (self.pv.count,)), st.value
+
+    def train_capture(self, which: int) -> np.ndarray:
+        """Capture `which` (0 LN outputs, 1 relu'd hidden, 2 dh, 3 dV) of the last
+        train minibatch as [layers][B][cols]: float32 in fp32 mode; in bf16 mode
+        the bfloat16 values unpacked from the row-group-packed layout, as float32."""
+        p, rows, cols, layers = C.c_void_p(), u32(), u32(), u32()
+        check(lib().mg_ppo_train_capture(self.h, which, C.byref(p), C.byref(rows), C.byref(cols), C.byref(layers)))
+        Lr, B, Cc = layers.value, rows.value, cols.value
+        if self.pv.precision == 0:
+            return d2h(p.value, np.float32, (Lr, B, Cc))
+        raw = d2h(p.value, np.uint16, (Lr, B // 8, Cc, 8))
+        return (raw.astype(np.uint32) << 16).view(np.float32).transpose(0, 1, 3, 2).reshape(Lr, B, Cc)
 
     def set_log_std(self, value: float) -> None:
         check(lib().mg_ppo_set_log_std(self.h, value))

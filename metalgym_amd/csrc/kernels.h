@@ -20,7 +20,7 @@ int launch_adv_stats(hipStream_t st, const float* adv, uint32_t n, uint32_t hori
 
 // Everything one PPO minibatch update needs on the device.
 struct TrainWs {
-    float* x;         // [(L+1)][B][128] LN outputs
+    float* x;         // [L][B][128] LN outputs entering the blocks
     float* v;         // [L][B][H] relu'd hidden activations
     float* dhb;       // [L][B][128] gradients at the block outputs
     float* dvb;       // [L][B][H] masked hidden gradients

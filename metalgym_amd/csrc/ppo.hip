@@ -133,8 +133,7 @@ int ensure_train_ws(mg_ppo* p, uint32_t minibatches) {
         train_ws_bytes(p->pv, p->B, &bytes);
         int rc = device_alloc(&p->ws_base, bytes, "PPOModel train workspace");
         if (rc) return rc;
-        // partial sums of padding elements are never written and must read as 0;
-        // the last-block ticket starts at 0
+        // tile partials of padding elements are never written and must read as 0
         MG_HIP(hipMemsetAsync(p->ws_base, 0, bytes, p->gym->stream), "train workspace clear");
         train_ws_bind(p->pv, p->B, p->ws_base, &p->ws);
     }
@@ -182,10 +181,6 @@ int download_stats(mg_ppo* p, uint32_t count) {
 }  // namespace mg
 
 using namespace mg;
-
-extern "C" {
-
-}  // extern "C"
 
 namespace mg {
 namespace {
@@ -502,6 +497,19 @@ int mg_ppo_params_updated(mg_ppo* p) {
     int rc = launch_derive_blocks(p->gym->stream, p->pv);
     if (rc) return rc;
     MG_HIP(hipStreamSynchronize(p->gym->stream), "params_updated synchronize");
+    return MG_OK;
+}
+
+int mg_ppo_train_capture(mg_ppo* p, uint32_t which, const void** ptr, uint32_t* rows, uint32_t* cols,
+                         uint32_t* layers) {
+    MG_CHECK(p && ptr && rows && cols && layers, MG_ERR_INVALID, "train_capture: null argument");
+    MG_CHECK(p->ws_base, MG_ERR_STATE, "train_capture: no train call yet");
+    const float* bufs[4] = {p->ws.x, p->ws.v, p->ws.dhb, p->ws.dvb};
+    MG_CHECK(which < 4, MG_ERR_INVALID, "train_capture: unknown capture %u", which);
+    *ptr = bufs[which];
+    *rows = p->B;
+    *cols = (which & 1) ? p->pv.hidden : MG_EMBED;
+    *layers = p->pv.layers;
     return MG_OK;
 }
 

@@ -471,8 +471,11 @@ struct Acts {
     }
 };
 
+// relu_mask ([L][H], nullable) replaces the ReLU's decision v > 0 for this
+// row: a unit passes (v = z) where the mask is 1 and is 0 where it is 0.
+// z_out ([L][H], nullable) receives the pre-activations z.
 void forward_row(const Net& n, const float* obs, float* head, float* xn_out, float* x_out, float* sd_out,
-                 float* v_out) {
+                 float* v_out, const uint8_t* relu_mask = nullptr, float* z_out = nullptr) {
     const uint32_t E = n.E, H = n.H;
     std::vector<float> h(E), xn(E), x(E), v(H), out(E);
     // model/input.metal:11-27: acc = bias, then obs . W in k order
@@ -500,7 +503,11 @@ void forward_row(const Net& n, const float* obs, float* head, float* xn_out, flo
             else
                 for (uint32_t j = 0; j < H; ++j) v[j] += xk * row[j];
         }
-        for (uint32_t j = 0; j < H; ++j) v[j] = v[j] > 0.0f ? v[j] : 0.0f;
+        if (z_out) std::memcpy(z_out + (size_t)l * H, v.data(), H * 4);
+        if (relu_mask)
+            for (uint32_t j = 0; j < H; ++j) v[j] = relu_mask[(size_t)l * H + j] ? v[j] : 0.0f;
+        else
+            for (uint32_t j = 0; j < H; ++j) v[j] = v[j] > 0.0f ? v[j] : 0.0f;
         if (v_out)  // the down GEMM's operand (rounded in bf16 mode), for dDown and the relu mask
             for (uint32_t j = 0; j < H; ++j) v_out[(size_t)l * H + j] = bf ? round_bf16(v[j]) : v[j];
         // model/mlp.metal:60-86: Out = V Down (bf16 operands: V and Down rounded);
@@ -821,6 +828,14 @@ void orc_collect(int env, const orc_dims* d, const float* params, uint32_t n, ui
 void orc_train_minibatch(const orc_dims* dp, const orc_hparams* hp, float* P, float* M, float* V, uint32_t step,
                          uint32_t B, const float* obs, const void* actions, const float* adv, const float* ret,
                          const float* old_logp, float* grad_out, orc_stats* stats, float* head_out, int threads) {
+    orc_train_minibatch_masked(dp, hp, P, M, V, step, B, obs, actions, adv, ret, old_logp, grad_out, stats, head_out,
+                               nullptr, nullptr, threads);
+}
+
+void orc_train_minibatch_masked(const orc_dims* dp, const orc_hparams* hp, float* P, float* M, float* V,
+                                uint32_t step, uint32_t B, const float* obs, const void* actions, const float* adv,
+                                const float* ret, const float* old_logp, float* grad_out, orc_stats* stats,
+                                float* head_out, const uint8_t* relu_mask, float* preact_out, int threads) {
     const orc_dims& d = *dp;
     Net net(d, P);
     const orc_layout& L = net.L;
@@ -833,8 +848,15 @@ void orc_train_minibatch(const orc_dims* dp, const orc_hparams* hp, float* P, fl
     parallel_for(B, threads, [&](uint32_t b, uint32_t e) {
         for (uint32_t r = b; r < e; ++r)
             forward_row(net, obs + (size_t)r * O, &head[(size_t)r * HD], &xn[r * actW], &x[r * actW],
-                        &sd[(size_t)r * (NL + 1)], &vv[(size_t)r * NL * H]);
+                        &sd[(size_t)r * (NL + 1)], &vv[(size_t)r * NL * H],
+                        relu_mask ? relu_mask + (size_t)r * NL * H : nullptr,
+                        preact_out ? preact_out + (size_t)r * NL * H : nullptr);
     });
+    // the backward's relu derivative: the forward's decision (the mask, if given)
+    auto passes = [&](uint32_t r, uint32_t l, uint32_t j) {
+        const size_t k = ((size_t)r * NL + l) * H + j;
+        return relu_mask ? relu_mask[k] != 0 : vv[k] > 0.0f;
+    };
     if (head_out) std::memcpy(head_out, head.data(), head.size() * 4);
 
     // model/gae.metal:42-77 over the minibatch rows
@@ -943,12 +965,11 @@ void orc_train_minibatch(const orc_dims* dp, const orc_hparams* hp, float* P, fl
                 const float* dhq = &dhb[((size_t)r * NL + l) * E];
                 const float* Dn = P + L.off_down[l];
                 const float* Up = P + L.off_up[l];
-                const float* vrow = &vv[((size_t)r * NL + l) * H];
                 for (uint32_t j = 0; j < H; ++j) {  // model/mlp.metal:88-127
                     float acc = 0.0f;
                     const float* row = Dn + (size_t)j * E;
                     for (uint32_t c = 0; c < E; ++c) acc += dhq[c] * q(row[c]);
-                    dv[j] = q(vrow[j] > 0.0f ? acc : 0.0f);
+                    dv[j] = q(passes(r, (uint32_t)l, j) ? acc : 0.0f);
                 }
                 std::memcpy(&dvb[((size_t)r * NL + l) * H], dv.data(), H * 4);
                 for (uint32_t k = 0; k < E; ++k) {  // model/mlp.metal:131-153

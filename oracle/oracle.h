@@ -4,7 +4,12 @@
  * __graft_entry__.smoke() and by bench.py's cpu_baseline leg as the checker.
  * The product (libmetalgym_amd.so) never links, loads or calls it.
  *
- * Each function cites the reference file:line it restates. Deliberate
+ * Each function cites the reference file:line it restates. Every function is
+ * pinned by a check independent of its own loops (known answers, closed forms,
+ * textbook equations, torch float64 fixtures, replays composed of separately
+ * pinned pieces; tests/test_cpu_oracle.py, tests/test_cpu_sampling.py,
+ * tests/test_cpu_voxelnav.py), and tests/test_cpu_oracle_mutants.py shows the
+ * sampler and collect pins reject planted slips. Deliberate
  * differences from the reference (fp32 instead of bf16 storage, the seed hash,
  * uniform init, contiguous minibatch blocks, tanh force) are the build-defined
  * semantics the product implements too.
@@ -116,6 +121,17 @@ void orc_train_minibatch(const orc_dims* d, const orc_hparams* hp, float* params
                          uint32_t step, uint32_t rows, const float* obs, const void* actions, const float* adv,
                          const float* ret, const float* old_logp, float* grad, orc_stats* stats, float* head_out,
                          int threads);
+
+/* orc_train_minibatch with the forward's ReLU decisions given: relu_mask
+ * ([rows][layers][hidden], 1 = the unit passes its pre-activation, nullable)
+ * replaces the test z > 0 in the forward and in the backward's mask, so the
+ * oracle evaluates the same piecewise-linear function as a run whose
+ * summation order put a pre-activation within rounding of 0 on the other side.
+ * preact_out ([rows][layers][hidden], nullable) receives the pre-activations. */
+void orc_train_minibatch_masked(const orc_dims* d, const orc_hparams* hp, float* params, float* m, float* v,
+                                uint32_t step, uint32_t rows, const float* obs, const void* actions, const float* adv,
+                                const float* ret, const float* old_logp, float* grad, orc_stats* stats,
+                                float* head_out, const uint8_t* relu_mask, float* preact_out, int threads);
 
 /* The build's minibatch order (D5): per epoch a Fisher-Yates shuffle of the
  * block ids driven by the model's shuffle stream. */

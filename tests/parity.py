@@ -64,3 +64,77 @@ def assert_close_bf16(got, want, what):
     assert p99 <= TOL_BF16_P99, f"{what}: 99th percentile scaled error {p99:.3g} > {TOL_BF16_P99}"
     assert worst <= TOL_BF16_MAX, f"{what}: max scaled error {worst:.3g} > {TOL_BF16_MAX}"
     return worst
+
+
+def group_errors(pv, a, b):
+    """Relative L2 error per parameter group (canonical layout offsets)."""
+    L, E, H, HD = pv.layers, pv.embed, pv.hidden, pv.head_dim
+    groups = {"in_w": (pv.off_in_w, pv.obs_dim * E), "in_b": (pv.off_in_b, E), "head": (pv.off_head, E * HD)}
+    for l in range(L + 1):
+        groups[f"ln{l}_gamma"] = (pv.off_ln_gamma[l], E)
+        groups[f"ln{l}_beta"] = (pv.off_ln_beta[l], E)
+    for l in range(L):
+        groups[f"up{l}"] = (pv.off_up[l], E * H)
+        groups[f"down{l}"] = (pv.off_down[l], H * E)
+    if pv.continuous:
+        groups["log_std"] = (pv.off_log_std, pv.act_dim)
+    out = {}
+    for k, (o, c) in groups.items():
+        x, y = a[o:o + c].astype(np.float64), b[o:o + c].astype(np.float64)
+        out[k] = float(np.linalg.norm(x - y) / max(np.linalg.norm(y), 1e-30))
+    return out
+
+
+TOL_MOMENT = 1e-3   # Adam moments per parameter group, relative L2, against the mask-matched oracle
+TOL_FLIP = 1e-5     # |z| of a flipped ReLU unit relative to ||x_row|| ||Up[:, j]||
+
+
+def check_minibatch(model, orc, d, hp, p0, rows, B, step=1):
+    """One fp32 minibatch update of the GPU against the oracle evaluating the
+    same function: the oracle replays the GPU's ReLU decisions (read from the
+    row pass's hidden capture), so a pre-activation that two summation orders
+    put on either side of 0 counts as the same unit. Then, with no exemptions:
+    - the recomputed head within TOL_HEAD;
+    - both Adam moments of every parameter group within TOL_MOMENT relative L2
+      (after one step from zero moments they are 0.1 g and 0.001 g^2 of the
+      clipped gradient, so this holds the gradient itself);
+    - every flipped unit's pre-activation is within rounding of 0: |z| <=
+      TOL_FLIP ||x_row|| ||Up[:, j]||, z as the oracle computes it;
+    - LossStats within TOL_TRAIN (clip_frac within two rows) and the post-Adam
+      weights within TOL_TRAIN.
+    Returns the oracle's (stats, params) after the step."""
+    pv = model.pv
+    m1, v1, st_gpu = model.adam_state()
+    assert st_gpu == step
+    hid = model.train_capture(1)  # [L][B][H]
+    x = model.train_capture(0)    # [L][B][E]
+    mask = np.ascontiguousarray((hid > 0).transpose(1, 0, 2))
+    P, M, V = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    st, grad, head, pre = orc.train_minibatch_masked(d, hp, P, M, V, step, *rows, mask, threads=THREADS)
+    assert_close(model.head(), head, TOL_HEAD, "recomputed head")
+    em, ev = group_errors(pv, m1, M), group_errors(pv, v1, V)
+    flips = (pre > 0) != mask
+    nflip = int(flips.sum())
+    worst = 0.0
+    if nflip:
+        r, l, j = np.nonzero(flips)
+        E, H = pv.embed, pv.hidden
+        upn = np.stack([np.linalg.norm(p0[pv.off_up[k]:pv.off_up[k] + E * H].reshape(E, H).astype(np.float64), axis=0)
+                        for k in range(pv.layers)])
+        scale = np.linalg.norm(x.transpose(1, 0, 2)[r, l].astype(np.float64), axis=-1) * upn[l, j]
+        rel = np.abs(pre[r, l, j]) / scale
+        worst = float(rel.max())
+    print(f"ReLU units on the other side of 0: {nflip} of {mask.size} (worst |z| / scale {worst:.2e}); "
+          f"moment m worst {max(em.values()):.2e} ({max(em, key=em.get)}), v worst {max(ev.values()):.2e}")
+    assert worst <= TOL_FLIP, f"a flipped ReLU unit's pre-activation is {worst:.3g} of its scale"
+    bad = {k: e for k, e in em.items() if e >= TOL_MOMENT}
+    assert not bad, f"first moment (gradient) differs: {bad}"
+    bad = {k: e for k, e in ev.items() if e >= TOL_MOMENT}
+    assert not bad, f"second moment differs: {bad}"
+    got, want = np.array(model.last_stats().as_tuple()), np.array(st.as_tuple())
+    assert_close(got[[0, 1, 2, 3, 5]], want[[0, 1, 2, 3, 5]], TOL_TRAIN, "LossStats")
+    assert abs(got[4] - want[4]) * B <= 2.0 + 1e-3, (got[4], want[4])
+    p1 = model.params()
+    assert_close(p1, P, TOL_TRAIN, "post-Adam weights")
+    assert np.all(np.isfinite(p1))
+    return st, P

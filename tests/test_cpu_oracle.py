@@ -472,3 +472,64 @@ def test_bf16_ppo_gradient_vs_torch(orc, name):
         print(f"{k}: bf16 oracle vs torch {e_bf:.2e}, fp32 oracle vs torch {e_fp:.2e}")
         assert e_bf < 1e-3, (k, e_bf)
         assert e_fp > 10 * e_bf, (k, e_fp, e_bf)
+
+
+@pytest.mark.parametrize("name", ["ppo_categorical", "ppo_gaussian"])
+def test_masked_train_step_vs_torch(orc, name):
+    """The oracle's ReLU-mask override (the GPU gradient gate replays the GPU's
+    ReLU decisions through it) against torch float64 autograd of the function
+    the mask defines: each block's hidden units are its pre-activations times
+    a fixed 0/1 mask. The mask is the oracle's own z > 0 with a few hundred
+    decisions inverted, including units far from 0, so a mask applied only in
+    the forward or only in the backward, or ignored, fails. With the mask equal
+    to z > 0 the step is bit for bit the unmasked one."""
+    import torch
+    import torch.nn.functional as F
+
+    from golden import make_golden as mk
+
+    z = load(name)
+    O, A, E, H, L, cont, B = (int(x) for x in z["dims"])
+    d = orc.Dims(O, A, E, H, L, cont, 0)
+    clip, vc, ec, mgn, gamma, lam, lr = z["hp"]
+    hp = orc.hparams(clip=clip, value_coef=vc, entropy_coef=ec, max_grad_norm=mgn, lr=lr)
+    args = (z["obs"], z["actions"], z["adv"], z["ret"], z["old_logp"])
+    fresh = lambda: (z["params0"].copy(), np.zeros_like(z["params0"]), np.zeros_like(z["params0"]))
+    P0, M0, V0 = fresh()
+    _, g_plain, _ = orc.train_minibatch(d, hp, P0, M0, V0, 1, *args, threads=2)
+    P1, M1, V1 = fresh()
+    _, g_own, _, pre = orc.train_minibatch_masked(d, hp, P1, M1, V1, 1, *args, None, threads=2)
+    P2, M2, V2 = fresh()
+    _, g_same, _, _ = orc.train_minibatch_masked(d, hp, P2, M2, V2, 1, *args, pre > 0, threads=2)
+    assert np.array_equal(g_plain, g_own) and np.array_equal(g_plain, g_same)
+    assert np.array_equal(P0, P2) and np.array_equal(M0, M2) and np.array_equal(V0, V2)
+    rs = np.random.default_rng(11)
+    mask = pre > 0
+    flip = rs.random(mask.shape) < 0.05
+    mask ^= flip
+    P3, M3, V3 = fresh()
+    _, g_mask, _, pre3 = orc.train_minibatch_masked(d, hp, P3, M3, V3, 1, *args, mask, threads=2)
+    # torch: the same network with relu(z) replaced by z * mask
+    t = mk.torch_params(z["params0"], O, A, E, H, L, bool(cont))
+    mt = torch.tensor(mask, dtype=torch.float64)
+    h = torch.tensor(z["obs"], dtype=torch.float64) @ t["in_w"] + t["in_b"]
+    zs = []
+    for l in range(L):
+        x = F.layer_norm(h, (E,), t[f"g{l}"], t[f"b{l}"], eps=1e-5)
+        zl = x @ t[f"up{l}"]
+        zs.append(zl.detach().numpy())
+        h = h + (zl * mt[:, l, :]) @ t[f"down{l}"]
+    x = F.layer_norm(h, (E,), t[f"g{L}"], t[f"b{L}"], eps=1e-5)
+    head = x @ t["head"]
+    act = torch.tensor(z["actions"], dtype=torch.float64 if cont else torch.int64)
+    f64 = lambda a: torch.tensor(a, dtype=torch.float64)
+    loss, _, _ = mk.ppo_loss(head, A, bool(cont), t, act, f64(z["adv"]), f64(z["ret"]), f64(z["old_logp"]), clip, vc,
+                             ec)
+    loss.backward()
+    off, count = mk.layout(O, A, E, H, L, bool(cont))
+    want = np.zeros(count)
+    for k, v in t.items():
+        want[off[k]:off[k] + v.numel()] = v.grad.numpy().ravel()
+    np.testing.assert_allclose(pre3, np.stack(zs, axis=1), rtol=1e-4, atol=1e-5)
+    assert rel_group_err(g_mask, want) < 2e-5
+    assert rel_group_err(g_plain, want) > 100 * rel_group_err(g_mask, want)

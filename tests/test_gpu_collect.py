@@ -68,14 +68,25 @@ def test_collect_teacher_forced(mg, orc, env, n, T):
     run_collect_parity(mg, orc, env, n, T)
 
 
-def test_collect_full_size_subset(mg, orc):
-    """The headline configuration (262144 CartPole envs, T = 32): two collects on
-    the GPU; the oracle replays 1536 of the envs (first, last and a random
-    spread) teacher-forced from the same seeds. Envs are independent, so the
-    subset must match bit for bit (values 1e-4); GAE is checked bit for bit over
-    all envs on the GPU's own inputs."""
-    eid, kernel = ENVS["cartpole"]
-    n, T = 262144, 32
+@pytest.mark.parametrize("env,n,block", [
+    ("cartpole", 262144, 37),              # config 2 (the headline) and config 3
+    ("cartpole_continuous", 65536, 21),    # config 4
+    ("cartpole_continuous", 262144, 1999),
+    ("voxelnav16", 262144, 1000),          # config 5
+])
+def test_collect_full_size_subset(mg, orc, env, n, block):
+    """A benchmarked configuration at its full size (T = 32): two collects on
+    the GPU; the oracle replays 1536 of the envs (first, last, tile edges and a
+    random spread) teacher-forced from the same seeds. Envs are independent, so
+    the subset must match bit for bit (values 1e-4); GAE is checked bit for
+    bit over all envs on the GPU's own inputs. Then one 4096-row minibatch of
+    the full-size rollout (the benchmark's minibatch shape) against the
+    oracle's train step, with the GPU's ReLU decisions replayed."""
+    from parity import check_minibatch
+    from test_gpu_train import block_rows
+
+    eid, kernel = ENVS[env]
+    T, B = 32, 4096
     gym = mg.Gym(kernel, n, 0)
     model = mg.PPOModel(gym, horizon=T)
     d = orc.dims(eid)
@@ -88,13 +99,14 @@ def test_collect_full_size_subset(mg, orc):
     g.state[:] = full.state.reshape(n, sb)[idx].ravel()
     g.rng[:] = full.rng[idx]
     g.done[:] = full.done[idx]
+    del full
     slots = orc.Slots(eid, idx.size, T)
     for c in range(2):
         model.collect()
         s = model.download_slots()
         head = model.head()
         orc.collect(g, d, params, T, slots, first=(c == 0), teacher_actions=s["actions"][:, idx], threads=THREADS)
-        tag = f"262144-env collect {c}"
+        tag = f"{n}-env {env} collect {c}"
         assert_bit_exact(s["obs"][:, idx], slots.obs, f"{tag} obs slots")
         assert_bit_exact(s["reward"][:, idx], slots.reward, f"{tag} rewards")
         assert_bit_exact(s["done"][:, idx], slots.done, f"{tag} dones")
@@ -107,6 +119,9 @@ def test_collect_full_size_subset(mg, orc):
         assert_bit_exact(s["adv"], adv, f"{tag} advantages")
         assert_bit_exact(s["ret"], ret, f"{tag} returns")
     assert np.isfinite(s["value"]).all() and np.isfinite(s["logp"]).all()
+    p0 = model.params()
+    model.train_block(block)
+    check_minibatch(model, orc, d, orc.hparams(), p0, block_rows(s, n, B, block), B)
 
 
 @pytest.mark.parametrize("n,T,layers,scale", [

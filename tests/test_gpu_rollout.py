@@ -91,3 +91,39 @@ def test_large_random_rollout_invariants(mg):
     assert np.array_equal(dn.astype(bool), term)  # no truncation within 32 steps of a fresh start
     # each env's actions are roughly fair coin flips
     assert abs(acts.mean() - 0.5) < 0.01
+
+
+@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "voxelnav16"])
+def test_step_into_slot_buffers(mg, orc, env):
+    """Gym::stepInto (gym.h:94-108, encodeStep): T single steps, step t reading
+    slot t of a device action buffer and writing slot t of device obs and
+    reward buffers (each at its own offset, as collect writes obs[t + 1]),
+    bit for bit against the oracle's given-action rollout; the gym's state,
+    RNG and done flags too, and slots beyond the written ones stay untouched."""
+    eid, kernel = ENVS[env]
+    n, T = 1536, 24
+    gym = mg.Gym(kernel, n, 4)
+    g = orc.GymState(eid, n, 4)
+    rs = np.random.default_rng(8)
+    if gym.continuous:
+        acts = (rs.standard_normal((T, n, gym.act_dim)) * 2).astype(np.float32)
+    else:
+        acts = rs.integers(0, gym.act_dim, (T, n)).astype(np.int32)
+    abuf = mg.DeviceBuffer.from_array(acts)
+    obs_sentinel = np.full((T + 1, n, gym.obs_dim), -7.0, np.float32)
+    rew_sentinel = np.full((T + 1, n), -7.0, np.float32)
+    obuf = mg.DeviceBuffer.from_array(obs_sentinel)
+    rbuf = mg.DeviceBuffer.from_array(rew_sentinel)
+    for t in range(T):  # obs into slot t + 1, reward into slot t, as in collect
+        gym.step_into(abuf.ptr + t * n * gym.action_bytes, obuf.ptr + (t + 1) * n * gym.obs_dim * 4,
+                      rbuf.ptr + t * n * 4)
+    gym.sync()
+    obs = obuf.download(np.float32, (T + 1, n, gym.obs_dim))
+    rew = rbuf.download(np.float32, (T + 1, n))
+    _, oo, orw, od = orc.rollout(g, T, random=False, actions_in=acts, threads=THREADS)
+    assert_bit_exact(obs[1:], oo, "obs")
+    assert_bit_exact(rew[:T], orw, "reward")
+    assert np.all(obs[0] == -7.0) and np.all(rew[T] == -7.0), "step_into wrote outside its slots"
+    compare_gym(gym, g, env)
+    if env != "voxelnav16":  # VoxelNav16 episodes last up to 256 steps; the first step's resets still run
+        assert od.any(), "no episode ended: the test does not exercise resets"

@@ -5,16 +5,17 @@ library (tests/envs, registered with MG_DEFINE_ENV like a user's env). The
 oracle has no model of these envs' dynamics, so collect is checked on its
 policy side: the values, log-probabilities and bootstrap head the GPU wrote
 against the oracle's forward of the GPU's own observation slots (1e-4); the
-minibatch against the oracle's train step on the GPU's rollout (head 1e-4,
-post-Adam weights and LossStats 1e-3)."""
+minibatch against the oracle's train step on the GPU's rollout, with the
+GPU's ReLU decisions replayed (head 1e-4, Adam moments, post-Adam weights and
+LossStats 1e-3)."""
 import ctypes
 import os
 
 import numpy as np
 import pytest
 
-from parity import THREADS, TOL_HEAD, TOL_TRAIN, assert_bit_exact, assert_close
-from test_gpu_train import block_rows, check_moment
+from parity import THREADS, TOL_HEAD, assert_bit_exact, assert_close, check_minibatch
+from test_gpu_train import block_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -77,12 +78,4 @@ def test_wide_minibatch(wide, orc, cont):
     p0 = model.params()
     hp = orc.hparams()
     model.train_block(block)
-    P, M, V = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
-    st, grad, head = orc.train_minibatch(d, hp, P, M, V, 1, *block_rows(s, n, B, block), threads=THREADS)
-    assert_close(model.head(), head, TOL_HEAD, "recomputed head")
-    m1, _, _ = model.adam_state()
-    check_moment(model.pv, m1, M, p0, block_rows(s, n, B, block), hp)
-    assert_close(model.params(), P, TOL_TRAIN, "post-Adam weights")
-    got, want = np.array(model.last_stats().as_tuple()), np.array(st.as_tuple())
-    assert_close(got[[0, 1, 2, 3, 5]], want[[0, 1, 2, 3, 5]], TOL_TRAIN, "LossStats")
-    assert abs(got[4] - want[4]) * B <= 2.0 + 1e-3, (got[4], want[4])
+    check_minibatch(model, orc, d, hp, p0, block_rows(s, n, B, block), B)
