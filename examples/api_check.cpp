@@ -87,11 +87,19 @@ int main() {
         model.forward();
         std::mt19937 rng(1);
         model.act(rng);
+        uint32_t ones = 0;
         for (uint32_t i = 0; i < N; i++) {
-            CHECK(gym.actions()[i] == 0 || gym.actions()[i] == 1);
+            const int a = gym.actions()[i];
+            CHECK(a == 0 || a == 1);
+            ones += (uint32_t)a;
             CHECK(model.values()[i] == model.headValue(i, CartPole::ACT_DIM));
-            CHECK(model.logProbs()[i] < 0.0f);
+            // log-probability of the chosen action under the softmax of the head
+            const double z0 = model.headValue(i, 0), z1 = model.headValue(i, 1);
+            const double m = z0 > z1 ? z0 : z1;
+            const double lse = m + std::log(std::exp(z0 - m) + std::exp(z1 - m));
+            CHECK(std::fabs(model.logProbs()[i] - ((a ? z1 : z0) - lse)) < 1e-5);
         }
+        CHECK(ones > N / 4 && ones < 3 * N / 4);  // the initial policy is close to uniform
         model.actGreedy();
         for (uint32_t i = 0; i < N; i++) {
             const int best = model.headValue(i, 1) > model.headValue(i, 0) ? 1 : 0;
@@ -123,7 +131,21 @@ int main() {
         std::mt19937 rng(2);
         model.forward();
         model.act(rng);
-        CHECK(std::isfinite(gym.actions()[0].force));
+        // (action - mean) / std is the standard normal draw: sample moments over N rows
+        double s1 = 0.0, s2 = 0.0;
+        const float sd = std::exp(model.logStdValue(0));
+        for (uint32_t i = 0; i < N; i++) {
+            CHECK(std::isfinite(gym.actions()[i].force));
+            const double z = (gym.actions()[i].force - model.headValue(i, 0)) / sd;
+            s1 += z;
+            s2 += z * z;
+            const double lp = -0.5 * z * z - std::log(sd) - 0.5 * std::log(2.0 * M_PI);
+            CHECK(std::fabs(model.logProbs()[i] - lp) < 1e-4);
+        }
+        CHECK(std::fabs(s1 / N) < 4.0 / std::sqrt((double)N));
+        CHECK(std::fabs(s2 / N - 1.0) < 4.0 * std::sqrt(2.0 / N));
+        model.actGreedy();
+        for (uint32_t i = 0; i < N; i++) CHECK(gym.actions()[i].force == model.headValue(i, 0));
     }
     std::printf(failures ? "api_check FAILED (%d)\n" : "api_check ok\n", failures);
     return failures ? 1 : 0;

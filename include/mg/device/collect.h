@@ -52,9 +52,11 @@ struct LdsState {
     static constexpr uint32_t STRIDE = SD % 2 ? SD : SD + 1;   // odd dword stride
     static constexpr size_t BYTES = (size_t)M * STRIDE * 4;
     static constexpr int O = Env::OBS_DIM, HD = Env::ACT_DIM + 1;
+    // 256 bytes of headroom for the compiler's alignment padding between the
+    // two static LDS arrays
     static constexpr bool USE = !EnvTraits<Env>::STATE_IN_REGISTERS && sizeof(State) % 4 == 0 &&
                                 alignof(State) <= 4 &&
-                                sizeof(CollectSmem<M, O, HD, BF16>) + BYTES <=
+                                sizeof(CollectSmem<M, O, HD, BF16>) + BYTES + 256 <=
                                     (size_t)163840 / CollectShape<M, O>::MIN_WG;
 };
 
@@ -63,28 +65,23 @@ struct LdsState {
 // kernel's dynamic LDS: the embed, LN and head phases then read them without
 // an L2 round trip (at one workgroup per CU no other workgroup's MFMAs overlap
 // that latency; at two, 64-row tiles, it took the 262144-env CartPole collect
-// from 36.0 to 34.9 ms). Used when they fit beside the tile (and a staged
-// State) at the kernel's workgroups per CU; else the forward reads the arena.
-// Host and kernel evaluate the same predicate: the launch passes floats() * 4
-// bytes of dynamic LDS exactly when fits() holds.
+// from 36.0 to 35.4 ms). Used when they fit beside the kernel's static LDS at
+// its workgroups per CU; else the forward reads the arena. The launcher
+// decides from the static size the compiler gave the kernel (padding
+// included) and passes the decision as the kernel's second argument.
 template <typename Env, int M, bool BF16>
 struct SmallStage {
     static constexpr int O = Env::OBS_DIM, HD = Env::ACT_DIM + 1;
     static constexpr int WIN = O * kEmbed, BIN = kEmbed, WH = kEmbed * HD;
-    using LS = LdsState<Env, M, BF16>;
-    static constexpr size_t STATIC = sizeof(CollectSmem<M, O, HD, BF16>) + (LS::USE ? LS::BYTES : 0);
     __host__ __device__ static constexpr uint32_t floats(uint32_t layers) {
         return WIN + BIN + (layers + 1) * 2 * kEmbed + WH;
-    }
-    __host__ __device__ static constexpr bool fits(uint32_t layers) {
-        return STATIC + (size_t)floats(layers) * 4 <= (size_t)163840 / CollectShape<M, O>::MIN_WG;
     }
 };
 
 // BF16: the policy forward multiplies bfloat16 operands (policy_bf16.h).
 template <typename Env, int M, bool BF16>
 __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectShape<M, Env::OBS_DIM>::MIN_WG))
-    collect_kernel(const mg_collect_args a) {
+    collect_kernel(const mg_collect_args a, const uint32_t stage_small) {
     using Tr = EnvTraits<Env>;
     using State = typename Env::State;
     using Action = typename Env::Action;
@@ -95,7 +92,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     __shared__ CollectSmem<M, O, HD, BF16> sm;
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     using SS = SmallStage<Env, M, BF16>;
-    extern __shared__ float small_lds[];  // SS::floats(layers) floats when SS::fits(layers)
+    extern __shared__ float small_lds[];  // SS::floats(layers) floats when stage_small
     FwdRegs<M, CS::W> R;
 
     const int tid = threadIdx.x;
@@ -131,7 +128,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     SmallParams sp = small_params(a.policy);
     // a runtime choice: a template parameter instead (LDS instructions for the
     // small parameters) measured slower at 4096 and 262144 envs, fp32 and bf16
-    if (SS::fits(a.policy.layers)) {  // ordered before the forwards by the barrier below
+    if (stage_small) {  // ordered before the forwards by the barrier below
         const int lnf = (int)(a.policy.layers + 1) * 2 * kEmbed;
         float* win = small_lds;
         float* bin = win + SS::WIN;
@@ -216,12 +213,30 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     }
 }
 
+// The kernel's static LDS as the compiler laid it out (SIZE_MAX if the
+// runtime cannot tell, which turns the small-parameter staging off).
+template <typename Env, int M, bool BF16>
+size_t collect_static_lds() {
+    static const size_t bytes = [] {
+        hipFuncAttributes attr{};
+        if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&collect_kernel<Env, M, BF16>)) != hipSuccess) {
+            (void)hipGetLastError();  // not this launch's error
+            return (size_t)SIZE_MAX;
+        }
+        return (size_t)attr.sharedSizeBytes;
+    }();
+    return bytes;
+}
+
 template <typename Env, int M, bool BF16>
 void launch_collect_m(const mg_collect_args* a, hipStream_t st) {
     using SS = SmallStage<Env, M, BF16>;
-    const uint32_t L = a->policy.layers;
+    constexpr size_t kPerWg = (size_t)163840 / CollectShape<M, Env::OBS_DIM>::MIN_WG;  // LDS per workgroup
+    const size_t stat = collect_static_lds<Env, M, BF16>();
+    const size_t dyn = (size_t)SS::floats(a->policy.layers) * 4;
+    const bool stage = stat <= kPerWg && dyn <= kPerWg - stat;
     const dim3 grid(a->n / M), block(CollectShape<M, Env::OBS_DIM>::NT);
-    hipLaunchKernelGGL((collect_kernel<Env, M, BF16>), grid, block, SS::fits(L) ? SS::floats(L) * 4 : 0, st, *a);
+    hipLaunchKernelGGL((collect_kernel<Env, M, BF16>), grid, block, stage ? dyn : 0, st, *a, stage ? 1u : 0u);
 }
 
 template <typename Env, bool BF16>

@@ -1,10 +1,10 @@
 // VoxelNav: the reference's heightmap navigation env
-// (examples/VoxelNav/voxelnav.metal:9-174), after minetrix's bridge task. A
-// 32 x 32 heightmap (uint8 heights, 0 = void) of rolling hills with one chasm
-// along z; the agent spawns on the near side, the goal is on the far side; it
-// walks, turns, jumps or places cobble to cross. The observation is a depth
-// camera of 8 x 4 rays marched through the heightmap plus the goal in the
-// agent's frame. Same State / Obs layout, constants, RNG draw order and
+// (examples/VoxelNav/voxelnav.metal:9-174). Terrain is a 32 x 32 grid of uint8
+// column heights (0 marks a hole); a trench of holes runs the length of the z
+// axis and separates the spawn region from the goal region. Six discrete
+// actions move, turn, leap two cells or drop a cobble block in front of the
+// agent. Each step it sees 32 depth samples (8 yaw angles x 4 pitch angles,
+// marched through the grid) and the goal's position relative to its heading. Same State / Obs layout, constants, RNG draw order and
 // arithmetic order as the reference; its Metal sin / cos are replaced by the
 // deterministic mg::sinf / mg::cosf so the host oracle and the GPU agree bit
 // for bit (the reference's own fast-math bits are not reproducible here).
@@ -39,9 +39,9 @@ struct VoxelNav {
         float prevDist;
         uint32_t steps;
         uint32_t cobble;
-        uint8_t height[W * W];  // terrain height per cell (x-major), 0 = void
+        uint8_t height[W * W];  // column height of cell (x, z) at x * W + z; 0 is a hole
     };
-    using Action = int;  // 0 forward, 1 back, 2 turn left, 3 turn right, 4 jump forward, 5 place cobble
+    using Action = int;  // 0 step ahead, 1 step back, 2 / 3 yaw -30 / +30 degrees, 4 leap 2 cells, 5 cobble
     struct Obs {
         float ray[N_RAYS];  // depth / MAX_DEPTH, ray c * RAY_ROWS + r
         float goalForward, goalRight, goalUp, goalDist;
@@ -62,7 +62,8 @@ struct VoxelNav {
     MG_HD static float mix(float x, float y, float a) { return x + (y - x) * a; }
 
     MG_HD static void reset(State& s, uint32_t& rng) {
-        // rolling hills: 5 x 5 random knots, bilinear between them
+        // base terrain: heights in [3, 9] on a 5 x 5 lattice, bilinearly
+        // interpolated to every cell and rounded
         float knot[25];
         for (uint32_t i = 0; i < 25; i++) knot[i] = rngUniform(rng, 3.0f, 9.0f);
         for (uint32_t cx = 0; cx < W; cx++) {
@@ -78,7 +79,8 @@ struct VoxelNav {
                 s.height[cell((int)cx, (int)cz)] = (uint8_t)roundf(h);
             }
         }
-        // one chasm along z, 2 to 5 cells wide; the far side may be lifted
+        // trench: columns left .. left + width - 1 (width 2-5) become holes, and
+        // every column past the trench is raised by 0-2 (capped at 15)
         const uint32_t width = 2 + rngInt(rng, 4);
         const uint32_t left = 12 + rngInt(rng, 6);
         const uint32_t lift = rngInt(rng, 3);
@@ -142,8 +144,9 @@ struct VoxelNav {
         o.height = h / 16.0f;
     }
 
-    // Moves to (nx, nz) if the target cell is solid and at most one block up;
-    // returns true if the move ended in the void.
+    // A move to (nx, nz): refused off the grid or onto a column more than one
+    // above the current one; onto a hole it is taken and reported (true) as a
+    // fall.
     MG_HD static bool tryMove(State& s, float nx, float nz) {
         const int cx = (int)floorf(nx), cz = (int)floorf(nz);
         if (!inside(cx, cz)) return false;

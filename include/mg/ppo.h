@@ -35,6 +35,7 @@ struct PPOModel {
                   "the Gaussian head needs an Action of exactly ACT_DIM floats");
     static constexpr float INIT_LOG_STD = 0.0f;
     static constexpr uint32_t HEAD_DIM = Env::ACT_DIM + 1;  // logits or means, then the value
+    static constexpr float kHalfLog2Pi = 0.9189385332046727f;  // ln(2 pi) / 2
     static_assert(Env::ACT_DIM + 1 <= 64, "ACT_DIM + value must fit a 64-wide head");
 
     Gym<Env>& gym;
@@ -104,67 +105,58 @@ struct PPOModel {
         headFresh_ = false;
     }
 
-    // model/ppo.h:636-684: host-side sampling from the last head into gym.actions().
+    // model/ppo.h:636-684: host-side sampling from the last head into
+    // gym.actions(), logProbs() and values(). The caller's generator is drawn
+    // in row order: one uniform per row for a discrete Action (inverse CDF of
+    // the softmax), one standard normal per action dimension for a float
+    // Action (mean + exp(log_std) z), as the reference draws it.
     template <typename Rng>
     void act(Rng& rng) {
         const float* head = headHost();
-        Action* action = gym.actions();
         if constexpr (CONTINUOUS) {
-            std::normal_distribution<float> normal(0.0f, 1.0f);
-            float* actionF = reinterpret_cast<float*>(action);
-            for (uint32_t row = 0; row < parallels; ++row) {
-                const size_t base = (size_t)row * HEAD_DIM;
-                float lp = 0.0f;
+            std::normal_distribution<float> stdNormal(0.0f, 1.0f);
+            float logStd[Env::ACT_DIM];
+            for (uint32_t k = 0; k < Env::ACT_DIM; ++k) logStd[k] = logStdValue(k);
+            float* out = reinterpret_cast<float*>(gym.actions());
+            for (uint32_t row = 0; row < parallels; ++row, out += Env::ACT_DIM) {
+                const float* mean = head + (size_t)row * HEAD_DIM;
+                float logDensity = 0.0f;
                 for (uint32_t k = 0; k < Env::ACT_DIM; ++k) {
-                    const float ls = logStdValue(k);
-                    const float mu = head[base + k];
-                    const float a = mu + std::exp(ls) * normal(rng);
-                    const float d = (a - mu) * std::exp(-ls);
-                    actionF[(size_t)row * Env::ACT_DIM + k] = a;
-                    lp += -0.5f * d * d - ls - 0.9189385332046727f;
+                    out[k] = mean[k] + std::exp(logStd[k]) * stdNormal(rng);
+                    const float z = (out[k] - mean[k]) * std::exp(-logStd[k]);  // the draw, recovered from the action
+                    logDensity += -0.5f * z * z - logStd[k] - kHalfLog2Pi;
                 }
-                logProbHost[row] = lp;
-                valueHost[row] = head[base + Env::ACT_DIM];
+                logProbHost[row] = logDensity;
+                valueHost[row] = mean[Env::ACT_DIM];
             }
         } else {
-            std::uniform_real_distribution<float> uniform(0.0f, 1.0f);
+            std::uniform_real_distribution<float> unit(0.0f, 1.0f);
+            float weight[Env::ACT_DIM];
             for (uint32_t row = 0; row < parallels; ++row) {
-                const float* z = head + (size_t)row * HEAD_DIM;
-                float rowMax = -INFINITY;
-                for (uint32_t a = 0; a < Env::ACT_DIM; ++a) rowMax = std::max(rowMax, z[a]);
-                float sum = 0.0f;
-                for (uint32_t a = 0; a < Env::ACT_DIM; ++a) sum += std::exp(z[a] - rowMax);
-                const float lse = rowMax + std::log(sum);
-                const float u = uniform(rng) * sum;
-                uint32_t chosen = Env::ACT_DIM - 1;
-                float acc = 0.0f;
-                for (uint32_t a = 0; a < Env::ACT_DIM; ++a) {
-                    acc += std::exp(z[a] - rowMax);
-                    if (u < acc) {
-                        chosen = a;
-                        break;
-                    }
+                const float* logit = head + (size_t)row * HEAD_DIM;
+                const float top = *std::max_element(logit, logit + Env::ACT_DIM);
+                float total = 0.0f;
+                for (uint32_t a = 0; a < Env::ACT_DIM; ++a) total += (weight[a] = std::exp(logit[a] - top));
+                // the first action whose cumulative weight exceeds u * total (the last if none does)
+                const float target = unit(rng) * total;
+                uint32_t pick = 0;
+                for (float cum = weight[0]; pick + 1 < Env::ACT_DIM && !(target < cum); cum += weight[++pick]) {
                 }
-                action[row] = (Action)chosen;
-                logProbHost[row] = z[chosen] - lse;
-                valueHost[row] = z[Env::ACT_DIM];
+                gym.actions()[row] = (Action)pick;
+                logProbHost[row] = logit[pick] - (top + std::log(total));
+                valueHost[row] = logit[Env::ACT_DIM];
             }
         }
     }
-    // model/ppo.h:686-702: argmax (discrete) or the mean (continuous).
+    // model/ppo.h:686-702: the most probable action (the first of equal ones), or the mean.
     void actGreedy() {
-        Action* action = gym.actions();
-        if constexpr (CONTINUOUS) {
-            float* actionF = reinterpret_cast<float*>(action);
-            for (uint32_t row = 0; row < parallels; ++row)
-                for (uint32_t k = 0; k < Env::ACT_DIM; ++k) actionF[(size_t)row * Env::ACT_DIM + k] = headValue(row, k);
-        } else {
-            for (uint32_t row = 0; row < parallels; ++row) {
-                uint32_t best = 0;
-                for (uint32_t a = 1; a < Env::ACT_DIM; ++a)
-                    if (headValue(row, a) > headValue(row, best)) best = a;
-                action[row] = (Action)best;
-            }
+        const float* head = headHost();
+        for (uint32_t row = 0; row < parallels; ++row) {
+            const float* h = head + (size_t)row * HEAD_DIM;
+            if constexpr (CONTINUOUS)
+                std::copy(h, h + Env::ACT_DIM, reinterpret_cast<float*>(gym.actions()) + (size_t)row * Env::ACT_DIM);
+            else
+                gym.actions()[row] = (Action)(std::max_element(h, h + Env::ACT_DIM) - h);
         }
     }
 
