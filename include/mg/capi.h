@@ -307,6 +307,20 @@ int mg_ppo_train(mg_ppo* model, uint32_t epochs);
  * (block b covers rows (b % (n / minibatch)) * minibatch ... of slot b / (n / minibatch)).
  * Blocking. */
 int mg_ppo_train_block(mg_ppo* model, uint32_t block);
+/* No reference counterpart: mg_ppo_train_block for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). The minibatch's workspace lives in a
+ * static device array of 64 MiB per device (held from library load to process
+ * exit), so the call makes no allocation; a policy whose workspace for one
+ * minibatch exceeds it (64 MiB minus 256 bytes; 60 MB for the 2-block, hidden
+ * 512 policy at 4096 rows) is rejected with MG_ERR_INVALID. The LossStats
+ * (6 floats, mg_loss_stats order) go to stats_out, a device pointer, or to
+ * the array when it is NULL. Asynchronous on the gym's stream; the Adam step
+ * count and its bias corrections are taken at call time. Every call on one
+ * device shares the array: calls that overlap on one device (two streams, two
+ * threads) race. mg_ppo_last_stats, mg_ppo_train_stats and
+ * mg_ppo_last_order are not updated. */
+int mg_ppo_train_block_noalloc(mg_ppo* model, uint32_t block, float* stats_out);
 /* model/ppo.h:628-634: policy forward on `rows` obs rows (device pointer) into
  * the model's head buffer. Blocking. */
 int mg_ppo_forward(mg_ppo* model, const float* obs, uint32_t rows);

@@ -131,6 +131,7 @@ def lib():
         "mg_ppo_train": (I, [P, u32]),
         "mg_ppo_train_block": (I, [P, u32]),
         "mg_ppo_forward": (I, [P, P, u32]),
+        "mg_ppo_train_block_noalloc": (I, [P, u32, P]),
         "mg_ppo_last_stats": (I, [P, P]),
         "mg_ppo_train_stats": (I, [P, P, u32, P]),
         "mg_ppo_slots_get": (I, [P, P]),
@@ -388,6 +389,11 @@ class PPOModel:
 
     def train_block(self, block: int) -> None:
         check(lib().mg_ppo_train_block(self.h, block))
+
+    def train_block_noalloc(self, block: int, stats_ptr: int = None) -> None:
+        """mg_ppo_train_block_noalloc: asynchronous; LossStats to the device
+        pointer stats_ptr (6 floats) if given."""
+        check(lib().mg_ppo_train_block_noalloc(self.h, block, stats_ptr))
 
     def forward(self, obs: np.ndarray) -> np.ndarray:
         obs = np.ascontiguousarray(obs, np.float32)

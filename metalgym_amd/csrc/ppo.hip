@@ -148,8 +148,9 @@ int ensure_train_ws(mg_ppo* p, uint32_t minibatches) {
     return MG_OK;
 }
 
-// One minibatch update on the stream (no host wait).
-int enqueue_minibatch(mg_ppo* p, uint32_t block, uint32_t mb_index) {
+// One minibatch update on the stream (no host wait), with workspace ws; the
+// minibatch's LossStats go to stats (6 floats, device).
+int enqueue_minibatch(mg_ppo* p, uint32_t block, uint32_t mb_index, const TrainWs& ws, float* stats) {
     const uint32_t perSlot = p->n / p->B;
     const uint32_t t = block / perSlot, r0 = (block % perSlot) * p->B;
     p->step += 1;
@@ -162,9 +163,50 @@ int enqueue_minibatch(mg_ppo* p, uint32_t block, uint32_t mb_index) {
     ts.mb_index = mb_index;
     ts.beta1_pow = powf(0.9f, stepF);
     ts.beta2_pow = powf(0.999f, stepF);
-    return launch_train_step(p->gym->stream, p->pv, p->hp, p->cfg.lr, p->ws, ts, p->obs_slots, p->action_slots,
-                             p->adv, p->ret, p->logp, p->adv_stats, p->m, p->v, p->head,
-                             p->mb_stats + (size_t)mb_index * 6);
+    return launch_train_step(p->gym->stream, p->pv, p->hp, p->cfg.lr, ws, ts, p->obs_slots, p->action_slots,
+                             p->adv, p->ret, p->logp, p->adv_stats, p->m, p->v, p->head, stats);
+}
+
+int enqueue_minibatch(mg_ppo* p, uint32_t block, uint32_t mb_index) {
+    return enqueue_minibatch(p, block, mb_index, p->ws, p->mb_stats + (size_t)mb_index * 6);
+}
+
+// ---- device memory of mg_ppo_train_block_noalloc -------------------------------
+// The train workspace of one minibatch and its LossStats in a file-scope
+// device array (below), which the HIP runtime places on every device that
+// loads the library and keeps until the process ends. Host code never uses
+// the array's name as an address: scratch_address() asks the runtime for the
+// array's address on the stream's device, once per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr size_t kNoAllocStatsBytes = 256;  // LossStats, at the array's start
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices];
+
+}  // namespace
+}  // namespace mg
+
+static __device__ __align__(256) unsigned char scratch[mg::kNoAllocScratchBytes];
+
+namespace mg {
+namespace {
+
+int scratch_address(hipStream_t st, unsigned char** out) {
+    hipDevice_t dev = 0;
+    MG_HIP(hipStreamGetDevice(st, &dev), "train_block_noalloc: stream device");
+    MG_CHECK(dev >= 0 && dev < kMaxDevices, MG_ERR_INVALID, "train_block_noalloc: device %d out of range", (int)dev);
+    if (!g_scratch[dev]) {
+        int cur = 0;
+        MG_HIP(hipGetDevice(&cur), "train_block_noalloc: current device");
+        if (cur != dev) MG_HIP(hipSetDevice(dev), "train_block_noalloc: select the stream's device");
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (cur != dev) MG_HIP(hipSetDevice(cur), "train_block_noalloc: restore the current device");
+        MG_HIP(e, "train_block_noalloc: scratch address");
+        MG_CHECK(ptr, MG_ERR_HIP, "train_block_noalloc: no scratch address");
+        g_scratch[dev] = ptr;
+    }
+    *out = static_cast<unsigned char*>(g_scratch[dev]);
+    return MG_OK;
 }
 
 int download_stats(mg_ppo* p, uint32_t count) {
@@ -424,6 +466,27 @@ int mg_ppo_train_block(mg_ppo* p, uint32_t block) {
     if ((rc = enqueue_minibatch(p, block, 0))) return rc;
     p->head_rows = p->B;
     return download_stats(p, 1);
+}
+
+int mg_ppo_train_block_noalloc(mg_ppo* p, uint32_t block, float* stats_out) {
+    MG_CHECK(p, MG_ERR_INVALID, "train_block_noalloc: null model");
+    MG_CHECK(p->collected, MG_ERR_STATE, "train_block_noalloc: call collect() first");
+    MG_CHECK(block < p->blocks, MG_ERR_INVALID, "train_block_noalloc: block %u out of range (%u blocks)", block,
+             p->blocks);
+    size_t need = 0;
+    train_ws_bytes(p->pv, p->B, &need);
+    MG_CHECK(need <= kNoAllocScratchBytes - kNoAllocStatsBytes, MG_ERR_INVALID,
+             "train_block_noalloc: a %u-row minibatch of this policy needs %zu bytes of workspace, more than the "
+             "%zu-byte static scratch (use mg_ppo_train_block)",
+             p->B, need, kNoAllocScratchBytes - kNoAllocStatsBytes);
+    unsigned char* base = nullptr;
+    int rc = scratch_address(p->gym->stream, &base);
+    if (rc) return rc;
+    TrainWs ws{};
+    train_ws_bind(p->pv, p->B, base + kNoAllocStatsBytes, &ws);
+    if ((rc = enqueue_minibatch(p, block, 0, ws, stats_out ? stats_out : reinterpret_cast<float*>(base)))) return rc;
+    p->head_rows = p->B;
+    return MG_OK;
 }
 
 int mg_ppo_forward(mg_ppo* p, const float* obs, uint32_t rows) {

@@ -495,10 +495,11 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     // model/linear.metal:71-93 on this tile: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
     // (sm.xs still holds the final LN output x_f)
     tile_outer<M, kTNT>(L.dhead, HD, HD, sm.xs, tp + pv.float_group, 1, HD);
-    if (pv.continuous && tid < A) {  // model/gaussian.metal:166-168, summed over the tile in row order
+    if (pv.continuous && tid < kEmbed) {  // model/gaussian.metal:166-168, summed over the tile in row order
         float s = 0.0f;
-        for (int r = 0; r < M; ++r) s += L.dls[r * A + tid];
-        tp[pv.off_log_std + tid] = s;
+        if (tid < A)
+            for (int r = 0; r < M; ++r) s += L.dls[r * A + tid];
+        tp[pv.off_log_std + tid] = s;  // and 0 in the arena padding after log_std (A <= 63 < 128)
     }
     if (tid >= 64 && tid < 64 + 5) {  // the tile's LossStats sums, in row order
         const int q = tid - 64;
