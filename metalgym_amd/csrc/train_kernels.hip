@@ -583,82 +583,176 @@ struct DwArgsT {
     float* partial;
 };
 
-constexpr int kDwRows = 32;    // rows staged in LDS per step
-constexpr int kDwLd = 64 + 4;  // LDS row stride of a staged 64-wide slab
+// The full gradient from its two sources, summed in fixed order, plus one
+// partial squared norm per workgroup:
+//  - workgroups [0, small_wgs): 16 tile-partial columns each (vector
+//    parameters, the head, then the 5 LossStats sums); 16 thread groups per
+//    column each add a range of tiles, and the ranges are added in order;
+//  - the rest: the block matrices, the sum of the row splits (grid-stride).
+constexpr int kRedCols = 16;  // tile-partial columns per small workgroup
+struct ReduceArgs {
+    const float* partial;
+    const float* tp;
+    float* grad;
+    float* normpart;
+    float* mb_stats;
+    uint32_t splits, tiles, tp_count, count;
+    uint32_t float_group, off_head, head_count, small_wgs;
+    float inv_rows;
+};
 
-// Workgroup id = tile * splits + split: workgroups go to the 8 XCDs round
-// robin, so with 8 or 16 splits all tiles of one row split run on the same XCD
-// and read its rows through that XCD's L2 (each row is fetched from memory
-// about once instead of once per tile sharing it).
-__global__ void __launch_bounds__(256) train_dw_kernel(const DwArgsT<float> a) {
-    __shared__ float xs[2][kDwRows * kDwLd];
-    __shared__ float ys[2][kDwRows * kDwLd];
+// Workgroup wg of nwg summing tile-partial columns (kRedCols at a time): NT /
+// kRedCols thread groups per column each add a range of tiles, and the ranges
+// are added in order. Writes the vector / head gradient and the minibatch
+// LossStats; returns this thread's sum of the squared gradient values it
+// wrote. NT threads.
+template <int NT>
+__device__ __forceinline__ float reduce_tile_partials(const ReduceArgs& a, uint32_t wg, uint32_t nwg) {
+    constexpr int NG = NT / kRedCols;  // thread groups per column
+    __shared__ float part[NG][kRedCols];
+    const int t = threadIdx.x;
+    float sq = 0.0f;
+    const uint32_t grp = t / kRedCols;
+    const uint32_t lo = grp * a.tiles / NG, hi = (grp + 1) * a.tiles / NG;
+    const uint32_t stat0 = a.float_group + a.head_count;
+    for (uint32_t c0 = wg * kRedCols; c0 < stat0 + 5; c0 += nwg * kRedCols) {
+        const uint32_t col = c0 + t % kRedCols;
+        float s = 0.0f;
+        if (col < stat0 + 5) {
+            const float* src = a.tp + col;
+            // loads issued eight at a time, added in tile order
+            for (uint32_t k0 = lo; k0 < hi; k0 += 8) {
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) x[u] = k0 + u < hi ? src[(size_t)(k0 + u) * a.tp_count] : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += x[u];
+            }
+        }
+        part[grp][t % kRedCols] = s;
+        __syncthreads();
+        if (t < kRedCols && col < stat0 + 5) {
+            float g = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NG; ++q) g += part[q][t];
+            if (col < a.float_group) {
+                a.grad[col] = g;
+                sq += g * g;
+            } else if (col < stat0) {
+                a.grad[a.off_head + (col - a.float_group)] = g;
+                sq += g * g;
+            } else {
+                a.mb_stats[col - stat0] = g * a.inv_rows;  // model/ppo.h:925-943 means
+            }
+        }
+        __syncthreads();
+    }
+    return sq;
+}
+
+// The workgroup's sum of sq to *out, in a fixed order (a DPP tree within each
+// wave, then the NW waves in order).
+template <int NW>
+__device__ __forceinline__ void write_norm_part(float sq, float* out) {
+    __shared__ float red[NW];
+    sq = group_sum<64>(sq);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = red[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) s += red[w];
+        *out = s;
+    }
+}
+
+constexpr int kDwRows = 64;             // rows staged in LDS per step
+constexpr int kDwTileM = 128;           // output tile: 128 x 64
+constexpr int kDwTileN = 64;
+constexpr int kDwLdX = kDwTileM + 4;    // LDS row strides of the staged slabs
+constexpr int kDwLdY = kDwTileN + 4;
+constexpr int kDwWaves = 8;             // two per SIMD
+
+// One 128 x 64 tile of a block matrix's gradient C = X^T Y over one row split:
+// 8 waves, wave w owning the 32 x 32 sub-tile at (32 (w / 2), 32 (w % 2)) as
+// one accumulator (v_mfma_f32_32x32x2_f32: A = X[k][m], B = Y[k][n] straight
+// from the staged slab, k = the rows). 64-row slabs of X (32 KB) and Y (16 KB)
+// are double-buffered in LDS, and each slab's loads are issued two slabs
+// before it is written there (two register sets), so one workgroup per CU
+// keeps two slabs of loads in flight; one barrier per slab. Workgroup id =
+// tile * splits + split: workgroups go to the 8 XCDs round robin, so with 8
+// or 16 splits all tiles of one row split run on the same XCD and share its
+// rows through that XCD's L2.
+__global__ void __launch_bounds__(64 * kDwWaves) train_dw_kernel(const DwArgsT<float> a) {
+    __shared__ float xs[2][kDwRows * kDwLdX];
+    __shared__ float ys[2][kDwRows * kDwLdY];
     const uint32_t split = blockIdx.x % a.splits, tile = blockIdx.x / a.splits;
     const uint32_t rowsPer = a.rows / a.splits;
     const uint32_t rb = split * rowsPer;
     float* out = a.partial + (size_t)split * a.count;
     const int tid = threadIdx.x;
-    if (tile < a.big_tiles) {
-        uint32_t t = tile, m = 0;
-        while (t >= a.tiles_per_big[m]) t -= a.tiles_per_big[m], ++m;
-        const BigMatT<float>& bm = a.big[m];
-        const uint32_t ntn = bm.ndim / 64;
-        const uint32_t tm = t / ntn, tn = t % ntn;
-        const int w = tid >> 6, lane = tid & 63, nn = lane & 31, hh = lane >> 5;
-        const int wm = 32 * (w >> 1), wn = 32 * (w & 1);  // this wave's 32x32 sub-tile
-        // staging: each thread moves two float4 of X and two of Y per 32-row slab;
-        // the next slab is loaded into registers before this slab's MFMAs and
-        // written to LDS after them, so its load latency hides behind the MFMAs
-        const int srow = tid >> 4, scol = (tid & 15) * 4;  // rows 0..15 (+16), columns 0..60
-        const float* xg = bm.x + (size_t)rb * bm.ldx + tm * 64 + scol;
-        const float* yg = bm.y + (size_t)rb * bm.ldy + tn * 64 + scol;
-        f32x4 px[2], py[2];
-        auto fetch = [&](uint32_t r0) {
+    uint32_t t = tile, m = 0;  // the grid is big_tiles * splits: every workgroup has a tile
+    while (t >= a.tiles_per_big[m]) t -= a.tiles_per_big[m], ++m;
+    const BigMatT<float>& bm = a.big[m];
+    const uint32_t ntn = bm.ndim / kDwTileN;
+    const uint32_t tm = t / ntn, tn = t % ntn;
+    const int w = tid >> 6, lane = tid & 63;
+    const int wm = 32 * (w >> 1), wn = 32 * (w & 1);
+    // staging: X rows t / 32 + 16 i (i < 4) at column 4 (t % 32); Y rows
+    // t / 16 + 32 i (i < 2) at column 4 (t % 16)
+    const int xr = tid >> 5, xc = 4 * (tid & 31), yr = tid >> 4, yc = 4 * (tid & 15);
+    const float* xg = bm.x + (size_t)(rb + xr) * bm.ldx + tm * kDwTileM + xc;
+    const float* yg = bm.y + (size_t)(rb + yr) * bm.ldy + tn * kDwTileN + yc;
+    // slab indices past the split's last slab reload the last one, so every
+    // step issues the same loads
+    f32x4 px[2][4], py[2][2];
+    const uint32_t steps = rowsPer / kDwRows;
+    auto fetch = [&](int set, uint32_t sl) {
+        const uint32_t r0 = (sl < steps ? sl : steps - 1) * kDwRows;
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const int rr = srow + 16 * h2;
-                px[h2] = *reinterpret_cast<const f32x4*>(xg + (size_t)(r0 + rr) * bm.ldx);
-                py[h2] = *reinterpret_cast<const f32x4*>(yg + (size_t)(r0 + rr) * bm.ldy);
-            }
-        };
-        auto put = [&](int buf) {
+        for (int i = 0; i < 4; ++i)
+            px[set][i] = *reinterpret_cast<const f32x4*>(xg + (size_t)(r0 + 16 * i) * bm.ldx);
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const int rr = srow + 16 * h2;
-                *reinterpret_cast<f32x4*>(&xs[buf][rr * kDwLd + scol]) = px[h2];
-                *reinterpret_cast<f32x4*>(&ys[buf][rr * kDwLd + scol]) = py[h2];
-            }
-        };
-        f32x16 acc = f32x16{};
-        const uint32_t steps = rowsPer / kDwRows;
-        fetch(0);
-        put(0);
+        for (int i = 0; i < 2; ++i)
+            py[set][i] = *reinterpret_cast<const f32x4*>(yg + (size_t)(r0 + 32 * i) * bm.ldy);
+    };
+    auto put = [&](int set, int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4*>(&xs[buf][(xr + 16 * i) * kDwLdX + xc]) = px[set][i];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) *reinterpret_cast<f32x4*>(&ys[buf][(yr + 32 * i) * kDwLdY + yc]) = py[set][i];
+    };
+    f32x16 acc = f32x16{};
+    // lane (i = l % 32, k = l / 32) supplies X[k][wm + i] and Y[k][wn + i]
+    const int ox = (lane >> 5) * kDwLdX + wm + (lane & 31), oy = (lane >> 5) * kDwLdY + wn + (lane & 31);
+    auto mfmas = [&](int buf) {
+        const float* xp = xs[buf] + ox;
+        const float* yp = ys[buf] + oy;
+#pragma unroll
+        for (int kk = 0; kk < kDwRows / 2; ++kk) acc = mfma32x32x2(xp[2 * kk * kDwLdX], yp[2 * kk * kDwLdY], acc);
+    };
+    // slab 0 in LDS buffer 0, slab 1 in set 1, slab 2 in set 0
+    fetch(0, 0);
+    fetch(1, 1);
+    put(0, 0);
+    fetch(0, 2);
+    __syncthreads();
+    for (uint32_t sl = 0; sl < steps; sl += 2) {
+        mfmas(0);      // slab sl
+        put(1, 1);     // slab sl + 1 (buffer 1 was last read before the previous barrier)
+        fetch(1, sl + 3);
         __syncthreads();
-        for (uint32_t s = 0; s < steps; ++s) {
-            const int cur = s & 1;
-            // every step loads (the last one reloads its own slab, unused), so the
-            // wait counts are the same on every iteration
-            fetch((s + 1 < steps ? s + 1 : s) * kDwRows);
-            const float* xc = xs[cur];
-            const float* yc = ys[cur];
-#pragma unroll
-            for (int g = 0; g < kDwRows / 8; ++g) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int k = 8 * g + 4 * hh + j;
-                    acc = mfma32x32x2(xc[k * kDwLd + wm + nn], yc[k * kDwLd + wn + nn], acc);
-                }
-            }
-            put(cur ^ 1);  // buffer cur ^ 1 was last read before the previous barrier
+        if (sl + 1 < steps) {
+            mfmas(1);  // slab sl + 1
+            put(0, 0); // slab sl + 2
+            fetch(0, sl + 4);
             __syncthreads();
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t row = tm * 64 + wm + c32_row(r, lane);
-            out[bm.off + (size_t)row * bm.ndim + tn * 64 + wn + nn] = acc[r];
-        }
-        return;
     }
+    float* o = out + bm.off + (size_t)(tm * kDwTileM + wm) * bm.ndim + tn * kDwTileN + wn + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[(size_t)c32_row(r, lane) * bm.ndim] = acc[r];
 }
 
 // The weight gradients with bf16 operands (MG_PRECISION_BF16). X and Y are
@@ -746,90 +840,6 @@ __global__ void __launch_bounds__(64 * NW) train_dw_bf16_kernel(const DwArgsT<ui
 #pragma unroll
         for (int q = 1; q < NW; ++q) v += red[q][e];
         out[(size_t)(e >> 6) * bm.ndim + (e & 63)] = v;
-    }
-}
-
-// The full gradient from its two sources, summed in fixed order, plus one
-// partial squared norm per workgroup:
-//  - workgroups [0, small_wgs): 16 tile-partial columns each (vector
-//    parameters, the head, then the 5 LossStats sums); 16 thread groups per
-//    column each add a range of tiles, and the ranges are added in order;
-//  - the rest: the block matrices, the sum of the row splits (grid-stride).
-constexpr int kRedCols = 16;  // tile-partial columns per small workgroup
-struct ReduceArgs {
-    const float* partial;
-    const float* tp;
-    float* grad;
-    float* normpart;
-    float* mb_stats;
-    uint32_t splits, tiles, tp_count, count;
-    uint32_t float_group, off_head, head_count, small_wgs;
-    float inv_rows;
-};
-
-// Workgroup wg of nwg summing tile-partial columns (kRedCols at a time): NT /
-// kRedCols thread groups per column each add a range of tiles, and the ranges
-// are added in order. Writes the vector / head gradient and the minibatch
-// LossStats; returns this thread's sum of the squared gradient values it
-// wrote. NT threads.
-template <int NT>
-__device__ __forceinline__ float reduce_tile_partials(const ReduceArgs& a, uint32_t wg, uint32_t nwg) {
-    constexpr int NG = NT / kRedCols;  // thread groups per column
-    __shared__ float part[NG][kRedCols];
-    const int t = threadIdx.x;
-    float sq = 0.0f;
-    const uint32_t grp = t / kRedCols;
-    const uint32_t lo = grp * a.tiles / NG, hi = (grp + 1) * a.tiles / NG;
-    const uint32_t stat0 = a.float_group + a.head_count;
-    for (uint32_t c0 = wg * kRedCols; c0 < stat0 + 5; c0 += nwg * kRedCols) {
-        const uint32_t col = c0 + t % kRedCols;
-        float s = 0.0f;
-        if (col < stat0 + 5) {
-            const float* src = a.tp + col;
-            // loads issued eight at a time, added in tile order
-            for (uint32_t k0 = lo; k0 < hi; k0 += 8) {
-                float x[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) x[u] = k0 + u < hi ? src[(size_t)(k0 + u) * a.tp_count] : 0.0f;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) s += x[u];
-            }
-        }
-        part[grp][t % kRedCols] = s;
-        __syncthreads();
-        if (t < kRedCols && col < stat0 + 5) {
-            float g = 0.0f;
-#pragma unroll
-            for (int q = 0; q < NG; ++q) g += part[q][t];
-            if (col < a.float_group) {
-                a.grad[col] = g;
-                sq += g * g;
-            } else if (col < stat0) {
-                a.grad[a.off_head + (col - a.float_group)] = g;
-                sq += g * g;
-            } else {
-                a.mb_stats[col - stat0] = g * a.inv_rows;  // model/ppo.h:925-943 means
-            }
-        }
-        __syncthreads();
-    }
-    return sq;
-}
-
-// The workgroup's sum of sq to *out, in a fixed order (a DPP tree within each
-// wave, then the NW waves in order).
-template <int NW>
-__device__ __forceinline__ void write_norm_part(float sq, float* out) {
-    __shared__ float red[NW];
-    sq = group_sum<64>(sq);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float s = red[0];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) s += red[w];
-        *out = s;
     }
 }
 
@@ -1216,7 +1226,9 @@ int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv) {
 // The weight-gradient jobs of one minibatch: per block, dUp and dDown from
 // the captures (T: their element type); tile x tile tiles.
 template <class T>
-dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B, uint32_t splits, uint32_t tile) {
+dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B, uint32_t splits, uint32_t tile,
+                        uint32_t tile_n = 0) {
+    if (!tile_n) tile_n = tile;
     const uint32_t E = MG_EMBED, H = pv.hidden;
     const T* x = reinterpret_cast<const T*>(ws.x);
     const T* v = reinterpret_cast<const T*>(ws.v);
@@ -1232,11 +1244,11 @@ dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B,
     for (uint32_t l = 0; l < pv.layers; ++l) {
         // dUp_l[k][j] = sum_r x_l[r][k] dV_l[r][j]  (model/mlp.metal:201-203)
         da.big[nb] = {x + (size_t)l * B * E, dv + (size_t)l * B * H, E, H, E, H, pv.off_up[l], 0};
-        da.tiles_per_big[nb] = (E / tile) * (H / tile);
+        da.tiles_per_big[nb] = (E / tile) * (H / tile_n);
         tiles += da.tiles_per_big[nb++];
         // dDown_l[j][c] = sum_r V_l[r][j] dh_l[r][c]  (model/mlp.metal:205-207)
         da.big[nb] = {v + (size_t)l * B * H, dh + (size_t)l * B * E, H, E, H, E, pv.off_down[l], 0};
-        da.tiles_per_big[nb] = (H / tile) * (E / tile);
+        da.tiles_per_big[nb] = (H / tile) * (E / tile_n);
         tiles += da.tiles_per_big[nb++];
     }
     da.nbig = nb;
@@ -1254,14 +1266,16 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
              "train: OBS_DIM <= 64 and ACT_DIM + 1 <= 64 required");
     const uint32_t E = MG_EMBED, L = pv.layers, H = pv.hidden;
     const bool bf = pv.precision == MG_PRECISION_BF16;
-    // 64 x 64 weight-gradient tiles over all block matrices
-    const uint32_t dw_tiles = 2 * L * (E / 64) * (H / 64);
+    // weight-gradient tiles over all block matrices: 128 x 64 (fp32) or 64 x 64 (bf16)
+    const uint32_t dw_tiles = bf ? 2 * L * (E / 64) * (H / 64) : 2 * L * (E * H / (dev::kDwTileM * dev::kDwTileN));
     // row splits of the block-matrix gradient sums: fp32, each split covers a
-    // multiple of 32 rows; bf16, a multiple of 64 rows and about two workgroups
-    // per CU in all (fewer splits, fewer partial sums to write and add)
+    // multiple of 32 rows and about one workgroup per CU in all; bf16, a
+    // multiple of 64 rows and about two workgroups per CU (fewer splits, fewer
+    // partial sums to write and add)
     const uint32_t split_rows = bf ? 16 * dev::kDwbWaves : dev::kDwRows;
+    const uint32_t max_wgs = bf ? 512 : 256;
     uint32_t splits = kSplits;
-    while (splits > 1 && (B % (splits * split_rows) != 0 || (bf && dw_tiles * splits > 512))) splits /= 2;
+    while (splits > 1 && (B % (splits * split_rows) != 0 || dw_tiles * splits > max_wgs)) splits /= 2;
     MG_CHECK(B % (splits * split_rows) == 0, MG_ERR_INVALID, "train: minibatch %u must be a multiple of %u", B,
              split_rows);
 
@@ -1323,8 +1337,9 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
                 hipLaunchKernelGGL((dev::train_dw_bf16_kernel<dev::kDwbWaves, 2>), dim3(dw_tiles * splits),
                                    dim3(64 * dev::kDwbWaves), 0, st, da);
             } else {
-                const auto da = dw_args<float>(pv, ws, B, splits, 64);
-                hipLaunchKernelGGL(dev::train_dw_kernel, dim3(dw_tiles * splits), dim3(256), 0, st, da);
+                const auto da = dw_args<float>(pv, ws, B, splits, dev::kDwTileM, dev::kDwTileN);
+                hipLaunchKernelGGL(dev::train_dw_kernel, dim3(dw_tiles * splits), dim3(64 * dev::kDwWaves), 0, st,
+                                   da);
             }
             MG_HIP(hipGetLastError(), "train dW launch");
         }
