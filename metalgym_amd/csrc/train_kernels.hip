@@ -110,12 +110,14 @@ struct LossIo {
 };
 
 // model/policy.metal:14-69 / model/gaussian.metal:76-135 for the tile's rows:
-// 32 threads per row (lrow, lk), thread lk owning head columns lk and lk + 32
-// (ACT_DIM <= 63), the row sums as group reductions. an, oldLp, ret, act are
-// the row's normalised advantage, old log-probability, return and action.
-// Also writes the recomputed head to a.head_out. No barrier.
+// TPR threads per row (lrow, lk), thread lk owning head columns lk + TPR u
+// (u < 64 / TPR; ACT_DIM + 1 <= 64), the row sums as group reductions. an,
+// oldLp, ret, act are the row's normalised advantage, old log-probability,
+// return and action. Also writes the recomputed head to a.head_out. No barrier.
+template <int TPR>
 __device__ __forceinline__ void loss_rows(const RowsArgs& a, const LossIo& io, int lrow, int lk, float an,
                                           float oldLp, float ret, int act, uint32_t r0, size_t g0) {
+    constexpr int NJ = 64 / TPR;  // head columns per thread
     const mg_policy_view& pv = a.pv;
     const int A = (int)pv.act_dim, HD = (int)pv.head_dim;
     const uint32_t B = a.step.rows;
@@ -123,58 +125,63 @@ __device__ __forceinline__ void loss_rows(const RowsArgs& a, const LossIo& io, i
     float* dz = io.dhead + lrow * HD;
     const float scale = 1.0f / (float)B;
     const float clip = a.hp.clip, ec = a.hp.entropy_coef;
-    const int j0 = lk, j1 = lk + 32;
-    const bool v0 = j0 < A, v1 = j1 < A;
     float entropy, logpA;
-    float d0 = 0.0f, d1 = 0.0f, is0 = 0.0f, is1 = 0.0f, p0 = 0.0f, p1 = 0.0f, lp0 = 0.0f, lp1 = 0.0f;
+    float dd[NJ], is[NJ], pr[NJ], lp[NJ];
+#pragma unroll
+    for (int u = 0; u < NJ; ++u) dd[u] = is[u] = pr[u] = lp[u] = 0.0f;
     if (!pv.continuous) {  // model/policy.metal:14-69
-        const float z0 = v0 ? h[j0] : -__builtin_huge_valf(), z1 = v1 ? h[j1] : -__builtin_huge_valf();
-        const float rowMax = group_max<32>(fmaxf(z0, z1));
-        float e = v0 ? fast_exp(z0 - rowMax) : 0.0f;
-        if (v1) e += fast_exp(z1 - rowMax);
-        const float lse = rowMax + fast_log(group_sum<32>(e));
+        float z[NJ], zmax = -__builtin_huge_valf();
+#pragma unroll
+        for (int u = 0; u < NJ; ++u) {
+            const int j = lk + TPR * u;
+            z[u] = j < A ? h[j] : -__builtin_huge_valf();
+            zmax = fmaxf(zmax, z[u]);
+        }
+        const float rowMax = group_max<TPR>(zmax);
+        float e = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NJ; ++u)
+            if (lk + TPR * u < A) e += fast_exp(z[u] - rowMax);
+        const float lse = rowMax + fast_log(group_sum<TPR>(e));
         float ent = 0.0f;
-        if (v0) lp0 = z0 - lse, p0 = fast_exp(lp0), ent -= p0 * lp0;
-        if (v1) lp1 = z1 - lse, p1 = fast_exp(lp1), ent -= p1 * lp1;
-        entropy = group_sum<32>(ent);
+#pragma unroll
+        for (int u = 0; u < NJ; ++u)
+            if (lk + TPR * u < A) lp[u] = z[u] - lse, pr[u] = fast_exp(lp[u]), ent -= pr[u] * lp[u];
+        entropy = group_sum<TPR>(ent);
         logpA = h[act] - lse;
     } else {  // model/gaussian.metal:76-135
         const float* actg = static_cast<const float*>(a.action_slots) + (g0 + lrow) * A;
         const float* logStd = pv.params + pv.off_log_std;
-        float lp = 0.0f, ent = 0.0f;
-        if (v0) {
-            const float ls = logStd[j0];
-            is0 = fast_exp(-ls);
-            d0 = (actg[j0] - h[j0]) * is0;
-            lp += -0.5f * d0 * d0 - ls - kLogSqrt2Pi;
-            ent += ls + kLogSqrt2Pi + 0.5f;
+        float lpa = 0.0f, ent = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NJ; ++u) {
+            const int j = lk + TPR * u;
+            if (j < A) {
+                const float ls = logStd[j];
+                is[u] = fast_exp(-ls);
+                dd[u] = (actg[j] - h[j]) * is[u];
+                lpa += -0.5f * dd[u] * dd[u] - ls - kLogSqrt2Pi;
+                ent += ls + kLogSqrt2Pi + 0.5f;
+            }
         }
-        if (v1) {
-            const float ls = logStd[j1];
-            is1 = fast_exp(-ls);
-            d1 = (actg[j1] - h[j1]) * is1;
-            lp += -0.5f * d1 * d1 - ls - kLogSqrt2Pi;
-            ent += ls + kLogSqrt2Pi + 0.5f;
-        }
-        logpA = group_sum<32>(lp);
-        entropy = group_sum<32>(ent);
+        logpA = group_sum<TPR>(lpa);
+        entropy = group_sum<TPR>(ent);
     }
     const float ratio = fast_exp(logpA - oldLp);
     const float surr1 = ratio * an;
     const float cr = fminf(fmaxf(ratio, 1.0f - clip), 1.0f + clip);
     const float surr2 = cr * an;
     const float gLogp = (surr1 <= surr2) ? -an * ratio : 0.0f;
-    if (!pv.continuous) {
-        if (v0) dz[j0] = (gLogp * ((j0 == act ? 1.0f : 0.0f) - p0) + ec * p0 * (lp0 + entropy)) * scale;
-        if (v1) dz[j1] = (gLogp * ((j1 == act ? 1.0f : 0.0f) - p1) + ec * p1 * (lp1 + entropy)) * scale;
-    } else {
-        if (v0) {
-            dz[j0] = gLogp * d0 * is0 * scale;
-            io.dls[lrow * A + j0] = (gLogp * (d0 * d0 - 1.0f) - ec) * scale;
-        }
-        if (v1) {
-            dz[j1] = gLogp * d1 * is1 * scale;
-            io.dls[lrow * A + j1] = (gLogp * (d1 * d1 - 1.0f) - ec) * scale;
+#pragma unroll
+    for (int u = 0; u < NJ; ++u) {
+        const int j = lk + TPR * u;
+        if (j < A) {
+            if (!pv.continuous) {
+                dz[j] = (gLogp * ((j == act ? 1.0f : 0.0f) - pr[u]) + ec * pr[u] * (lp[u] + entropy)) * scale;
+            } else {
+                dz[j] = gLogp * dd[u] * is[u] * scale;
+                io.dls[lrow * A + j] = (gLogp * (dd[u] * dd[u] - 1.0f) - ec) * scale;
+            }
         }
     }
     if (lk == 0) {
@@ -188,8 +195,11 @@ __device__ __forceinline__ void loss_rows(const RowsArgs& a, const LossIo& io, i
         st[4] = (fabsf(ratio - 1.0f) > clip) ? 1.0f : 0.0f;
     }
     if (a.head_out) {
-        if (j0 < HD) a.head_out[(size_t)(r0 + lrow) * HD + j0] = h[j0];
-        if (j1 < HD) a.head_out[(size_t)(r0 + lrow) * HD + j1] = h[j1];
+#pragma unroll
+        for (int u = 0; u < NJ; ++u) {
+            const int j = lk + TPR * u;
+            if (j < HD) a.head_out[(size_t)(r0 + lrow) * HD + j] = h[j];
+        }
     }
 }
 
@@ -510,7 +520,7 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     // ---- loss and head gradient: 32 threads per row, thread k owning head
     // columns k and k + 32 (ACT_DIM <= 63), the row sums as group reductions ----
     static_assert(kTNT == 32 * M && kMaxHeadT <= 64, "32 threads per row, two columns each");
-    loss_rows(a, LossIo{L.head, L.dhead, L.dls, L.stat}, lrow, lk, an, oldLp, ret, act, r0, g0);
+    loss_rows<32>(a, LossIo{L.head, L.dhead, L.dls, L.stat}, lrow, lk, an, oldLp, ret, act, r0, g0);
     __syncthreads();
 
     // model/linear.metal:71-93 on this tile: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
@@ -1295,8 +1305,10 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         ra.head_out = head_out;
         if (bf)
             hipLaunchKernelGGL(dev::train_rows_kernel<true>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
-        else if (dev::rows_split_fits(pv))
-            hipLaunchKernelGGL(dev::train_rows_split_kernel, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
+        else if (dev::rows_split_waves(pv) == 8)
+            hipLaunchKernelGGL(dev::train_rows_split_kernel<8>, dim3(B / dev::kTR), dim3(64 * 8), 0, st, ra);
+        else if (dev::rows_split_waves(pv) == 4)
+            hipLaunchKernelGGL(dev::train_rows_split_kernel<4>, dim3(B / dev::kTR), dim3(64 * 4), 0, st, ra);
         else
             hipLaunchKernelGGL(dev::train_rows_kernel<false>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         MG_HIP(hipGetLastError(), "train rows launch");

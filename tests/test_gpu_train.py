@@ -37,8 +37,8 @@ def block_rows(s, n, B, block):
     ("voxelnav16", 1024, 2, 512, 1, 2, 4),
     ("voxelnav", 1024, 2, 512, 1, 2, 4),
     ("cartpole", 1024, 2, 512, 2, 3, 2),      # hidden 256, three blocks
-    ("cartpole", 1024, 2, 512, 1, 4, 2),      # four blocks: the most the split row pass takes
-    ("cartpole", 1024, 2, 512, 1, 5, 2),      # five blocks (the chunk-barrier row pass)
+    ("cartpole", 1024, 2, 512, 1, 4, 2),      # four blocks: the most the 8-wave split row pass takes
+    ("cartpole", 1024, 2, 512, 1, 5, 2),      # five blocks: the 4-wave split row pass
     ("cartpole", 1024, 2, 512, 0, 8, 1),      # the most blocks (MG_MAX_LAYERS), hidden 128
     ("cartpole", 1024, 2, 512, 1, 2, 8),      # the widest hidden layer (scale 8: 1024)
     ("cartpole", 1024, 2, 512, 1, 1, 2),      # one block, hidden 256
