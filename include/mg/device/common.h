@@ -30,6 +30,17 @@ __device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// 16 bytes per lane from a wave-uniform base: base + soff + voff bytes, as
+// buffer_load_dwordx4 with the base in a buffer resource (SGPRs), soff in an
+// SGPR and voff in a VGPR, so no per-load 64-bit address arithmetic runs on
+// the VALU beside the MFMAs. The resource has no meaningful size limit (the
+// callers' offsets stay inside their arrays by construction).
+__device__ __forceinline__ f32x4 buffer_load16(const void* base, uint32_t voff, uint32_t soff) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
 __device__ __forceinline__ int c32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 __device__ __forceinline__ int c16_row(int r, int lane) { return 4 * (lane >> 4) + r; }
 

@@ -137,28 +137,33 @@ struct FragSrc {
     uint32_t ld;
 };
 
-// This lane's float4 of k-group 0 for column tile ct of its wave's strip. The
-// strip's address is wave-uniform (scalar registers), so every weight load is
-// a scalar base plus the one per-lane offset 16 lane bytes.
+// The first element of column tile ct of this wave's strip (wave-uniform:
+// scalar registers).
 template <int M, int W>
-__device__ __forceinline__ const float* frag_lane(const FragSrc& f, int ct) {
+__device__ __forceinline__ const float* frag_strip(const FragSrc& f, int ct) {
     using S = Shape<M, W>;
-    const uint32_t lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    return f.p + (size_t)(wave * S::CT + ct) * S::MT * f.ld + 4 * lane;
+    return f.p + (size_t)(wave * S::CT + ct) * S::MT * f.ld;
+}
+
+// This lane's float4 of k-group g of a strip: one 1 KB run per wave
+// instruction, a buffer load with the run's offset in a scalar register and
+// the per-lane 16 bytes as the only vector operand.
+__device__ __forceinline__ f32x4 frag_load(const float* strip, int g) {
+    return buffer_load16(strip, 16 * (threadIdx.x & 63), 1024 * g);
 }
 
 // Loads k-groups [g0, g0 + NG) of a fragment-tiled operand: one float4 per lane
-// and k-group, each wave instruction one 1 KB run.
+// and k-group.
 template <int M, int W, int NG>
 __device__ __forceinline__ void load_frag(BFrag<M, W, NG>& f, const FragSrc& src, int g0) {
     using S = Shape<M, W>;
 #pragma unroll
     for (int ct = 0; ct < S::CT; ++ct) {
-        const float* bp = frag_lane<M, W>(src, ct) + 256 * g0;
+        const float* strip = frag_strip<M, W>(src, ct);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(bp + 256 * g);
+            const f32x4 v = frag_load(strip, g0 + g);
 #pragma unroll
             for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
         }
@@ -275,7 +280,7 @@ struct TStream {
                         acc[rt][ct] = S::mfma(a[g][rt][j], b[ROLE].b[g][ct][j], acc[rt][ct]);
 #pragma unroll
             for (int ct = 0; ct < S::CT; ++ct) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(frag_lane<M, W>(f, ct) + 256 * g);
+                const f32x4 v = frag_load(frag_strip<M, W>(f, ct), g);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) b[ROLE].b[g][ct][j] = v[j];
             }

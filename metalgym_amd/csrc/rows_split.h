@@ -114,15 +114,19 @@ struct SkSeq {
 
 // The operand registers of both roles (8 S float4s each per lane): w0[8 s + g]
 // is k-group g of strip s, w1[S ct + s] strip s's k-group in column strip ct.
-// Each float4 is refilled for the same role of the next chunk right after its
-// MFMAs; past the end of the sequence a GEMM reloads its own operand, so every
-// path issues the same loads and the vector-memory wait counts stay exact.
+// The loads are buffer loads with the k-group offset in an SGPR: the 64-bit
+// address arithmetic of global loads ran on the VALU between the MFMAs and
+// cost 3 us of the fp32 row pass. Each float4 is refilled for the same role
+// of the next chunk right after its MFMAs; past the end of the sequence a GEMM
+// reloads its own operand, so every path issues the same loads and the
+// vector-memory wait counts stay exact.
 template <int S>
 struct SkStream {
     f32x4 w0[8 * S], w1[8 * S];
 
+    // one k-group: 16 bytes per lane of the 1 KB run at float offset off
     __device__ __forceinline__ static f32x4 load(const float* p, uint32_t off) {
-        return *reinterpret_cast<const f32x4*>(p + off + 4 * (threadIdx.x & 63));
+        return buffer_load16(p, 16 * (threadIdx.x & 63), 4 * off);
     }
     __device__ __forceinline__ void start(const SkSeq<S>& seq, const SkPos& p) {
         const float* a = seq.role0(p);
