@@ -46,8 +46,8 @@ struct TrainStep {
     float beta1_pow, beta2_pow;
 };
 
-// The fragment-tiled copies of the block matrices (frag_fwd32, frag_fwd16,
-// frag_bwd16) from params.
+// All fragment-tiled copies of the block matrices (frag_fwd32, frag_fwd16,
+// frag_bwd16 and the bf16 ones that exist) from params.
 int launch_derive_blocks(hipStream_t st, const mg_policy_view& pv);
 // MG_OK if the block matrices sit contiguously from float_group (the layout
 // the Adam and derive kernels tile).
@@ -55,7 +55,11 @@ int check_matrix_layout(const mg_policy_view& pv);
 
 int train_ws_bytes(const mg_policy_view& pv, uint32_t rows, size_t* bytes);
 int train_ws_bind(const mg_policy_view& pv, uint32_t rows, void* base, TrainWs* ws);
-// One minibatch: rows pass, weight-gradient pass, reduce + norm, Adam.
+// One minibatch: rows pass, weight-gradient pass, reduce + norm, Adam. Adam
+// rewrites only the fragment-tiled copies the row pass reads (frag_fwd16 and
+// frag_bwd16, or their bf16 versions in bf16 mode); the others (frag_fwd32
+// and, in bf16 mode, the fp32 copies and frag_fwd32_bf, read by collect and
+// forward) are stale afterwards until launch_derive_blocks.
 int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hparams& hp, float lr,
                       const TrainWs& ws, const TrainStep& step, const float* obs_slots, const void* action_slots,
                       const float* adv_slots, const float* ret_slots, const float* logp_slots,

@@ -35,6 +35,7 @@ struct mg_ppo {
     float* adv_stats = nullptr;
     bool rollout_started = false;
     bool collected = false;
+    bool tiles_stale = false;  // a train call left the copies that only collect and forward read behind params
     void* ws_base = nullptr;
     mg::TrainWs ws{};
     float* mb_stats = nullptr;
@@ -151,6 +152,7 @@ int ensure_train_ws(mg_ppo* p, uint32_t minibatches) {
 // One minibatch update on the stream (no host wait), with workspace ws; the
 // minibatch's LossStats go to stats (6 floats, device).
 int enqueue_minibatch(mg_ppo* p, uint32_t block, uint32_t mb_index, const TrainWs& ws, float* stats) {
+    p->tiles_stale = true;
     const uint32_t perSlot = p->n / p->B;
     const uint32_t t = block / perSlot, r0 = (block % perSlot) * p->B;
     p->step += 1;
@@ -165,6 +167,17 @@ int enqueue_minibatch(mg_ppo* p, uint32_t block, uint32_t mb_index, const TrainW
     ts.beta2_pow = powf(0.999f, stepF);
     return launch_train_step(p->gym->stream, p->pv, p->hp, p->cfg.lr, ws, ts, p->obs_slots, p->action_slots,
                              p->adv, p->ret, p->logp, p->adv_stats, p->m, p->v, p->head, stats);
+}
+
+// The fragment-tiled copies that the train kernels do not keep current
+// (launch_train_step), derived from params on the model's stream before a
+// kernel that reads them.
+int sync_tiles(mg_ppo* p) {
+    if (!p->tiles_stale) return MG_OK;
+    int rc = launch_derive_blocks(p->gym->stream, p->pv);
+    if (rc) return rc;
+    p->tiles_stale = false;
+    return MG_OK;
 }
 
 int enqueue_minibatch(mg_ppo* p, uint32_t block, uint32_t mb_index) {
@@ -398,6 +411,7 @@ int mg_ppo_get_hparams(mg_ppo* p, mg_ppo_hparams* hp) {
 int mg_ppo_collect(mg_ppo* p) {
     MG_CHECK(p, MG_ERR_INVALID, "collect: null model");
     hipStream_t st = p->gym->stream;
+    if (int rc = sync_tiles(p)) return rc;
     mg_collect_args a{};
     a.stream = st;
     a.policy = p->pv;
@@ -493,6 +507,7 @@ int mg_ppo_forward(mg_ppo* p, const float* obs, uint32_t rows) {
     MG_CHECK(p && (obs || rows == 0), MG_ERR_INVALID, "forward: null argument");
     int rc = ensure_head(p, rows);
     if (rc) return rc;
+    if ((rc = sync_tiles(p))) return rc;
     {
         TimedLaunch tl(MG_K_FORWARD, p->gym->stream);
         if ((rc = launch_forward(p->gym->stream, p->pv, obs, rows, p->head))) return rc;
@@ -542,6 +557,10 @@ int mg_ppo_head(mg_ppo* p, const float** head, uint32_t* rows, uint32_t* head_di
 
 int mg_ppo_policy(mg_ppo* p, mg_policy_view* out) {
     MG_CHECK(p && out, MG_ERR_INVALID, "policy: null argument");
+    if (p->tiles_stale) {  // the view's copies are current when it is handed out
+        if (int rc = sync_tiles(p)) return rc;
+        MG_HIP(hipStreamSynchronize(p->gym->stream), "policy synchronize");
+    }
     *out = p->pv;
     return MG_OK;
 }
@@ -559,6 +578,7 @@ int mg_ppo_params_updated(mg_ppo* p) {
     MG_CHECK(p, MG_ERR_INVALID, "params_updated: null model");
     int rc = launch_derive_blocks(p->gym->stream, p->pv);
     if (rc) return rc;
+    p->tiles_stale = false;
     MG_HIP(hipStreamSynchronize(p->gym->stream), "params_updated synchronize");
     return MG_OK;
 }

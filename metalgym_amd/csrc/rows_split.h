@@ -326,8 +326,15 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     const int n16 = lane & 15, q4 = 4 * (lane >> 4);
     float* tp = ws.tp + (size_t)blockIdx.x * ws.tp_count;
 
-    // start-up: every small array's first element per thread is loaded before
-    // any is stored, then the weight stream starts (train_rows_kernel's order)
+    // start-up: the weight stream's first loads, then every small array's
+    // first element per thread before any is stored, so the staging's one
+    // memory round trip overlaps the weights' instead of preceding it
+    const int rot = (wave + (int)(blockIdx.x >> 3)) % NC;
+    const SkSeq<S> seq{pv.frag_fwd16 + pv.float_group, pv.frag_bwd16 + pv.float_group, NL, NC, wave, rot,
+                       (uint32_t)kEmbed * (uint32_t)H};
+    SkPos pos{0, 0, 0};
+    SkStream<S> wst;
+    wst.start(seq, pos);
     float* const winL = &L.red[0][0];  // the partial buffer is unused until the first block's reduction
     float* const binL = winL + Sh::OBS * kEmbed;
     const float* lnp = pv.params + pv.off_ln_gamma[0];
@@ -360,12 +367,6 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         ret = a.ret_slots[gr];
         if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
     }
-    const int rot = (wave + (int)(blockIdx.x >> 3)) % NC;
-    const SkSeq<S> seq{pv.frag_fwd16 + pv.float_group, pv.frag_bwd16 + pv.float_group, NL, NC, wave, rot,
-                       (uint32_t)kEmbed * (uint32_t)H};
-    SkPos pos{0, 0, 0};
-    SkStream<S> wst;
-    wst.start(seq, pos);
     __syncthreads();
 
     float* const cx = ws.x;

@@ -1014,35 +1014,37 @@ __device__ __forceinline__ void store_tile_frags(const MatTile& m, const float* 
                                                  uint16_t* bwd16b) {
     __syncthreads();
     const int t = threadIdx.x;
-    {  // 32-wide strips: the tile is one strip's four k-groups, 4 KB in a row
+    if (fwd32) {  // 32-wide strips: the tile is one strip's four k-groups, 4 KB in a row
         const int n = t & 31, k = 8 * (t >> 6) + 4 * ((t >> 5) & 1);
         f32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = lds[(k + j) * kTileLd + n];
         *reinterpret_cast<f32x4*>(fwd32 + m.base + frag_index<32>(m.c0 + n, m.r0 + k, m.rows)) = v;
     }
-    const int n = 16 * (t >> 7) + (t & 15), k = 16 * ((t >> 6) & 1) + 4 * ((t >> 4) & 3);
-    f32x4 vb, vf;
+    if (fwd16 || bwd16) {
+        const int n = 16 * (t >> 7) + (t & 15), k = 16 * ((t >> 6) & 1) + 4 * ((t >> 4) & 3);
+        f32x4 vb, vf;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        vb[j] = lds[n * kTileLd + k + j];
-        vf[j] = lds[(k + j) * kTileLd + n];
+        for (int j = 0; j < 4; ++j) {
+            vb[j] = lds[n * kTileLd + k + j];
+            vf[j] = lds[(k + j) * kTileLd + n];
+        }
+        if (bwd16) *reinterpret_cast<f32x4*>(bwd16 + m.base + frag_index<16>(m.r0 + n, m.c0 + k, m.cols)) = vb;
+        if (fwd16) *reinterpret_cast<f32x4*>(fwd16 + m.base + frag_index<16>(m.c0 + n, m.r0 + k, m.rows)) = vf;
     }
-    *reinterpret_cast<f32x4*>(bwd16 + m.base + frag_index<16>(m.r0 + n, m.c0 + k, m.cols)) = vb;
-    *reinterpret_cast<f32x4*>(fwd16 + m.base + frag_index<16>(m.c0 + n, m.r0 + k, m.rows)) = vf;
-    if (fwd32b) {
-        if (t < 128) {
-            const int ln = t & 63, nb = ln & 31, kb = 16 * (t >> 6) + 8 * (ln >> 5);
+    if (t < 128) {
+        const int ln = t & 63, nb = ln & 31, kb = 16 * (t >> 6) + 8 * (ln >> 5);
+        if (fwd32b)
             *reinterpret_cast<u32x4*>(fwd32b + m.base + frag_index_b<32>(m.c0 + nb, m.r0 + kb, m.rows)) =
                 pack_bf16_column(lds, kb, nb);
-            const int nr = 16 * (t >> 6) + (ln & 15), kr = 8 * (ln >> 4);
+        const int nr = 16 * (t >> 6) + (ln & 15), kr = 8 * (ln >> 4);
+        if (bwd16b)
             *reinterpret_cast<u32x4*>(bwd16b + m.base + frag_index_b<16>(m.r0 + nr, m.c0 + kr, m.cols)) =
                 pack_bf16_row(lds, nr, kr);
-        } else {
-            const int t2 = t - 128, ln = t2 & 63, nb = 16 * (t2 >> 6) + (ln & 15), kb = 8 * (ln >> 4);
-            *reinterpret_cast<u32x4*>(fwd16b + m.base + frag_index_b<16>(m.c0 + nb, m.r0 + kb, m.rows)) =
-                pack_bf16_column(lds, kb, nb);
-        }
+    } else if (fwd16b) {
+        const int t2 = t - 128, ln = t2 & 63, nb = 16 * (t2 >> 6) + (ln & 15), kb = 8 * (ln >> 4);
+        *reinterpret_cast<u32x4*>(fwd16b + m.base + frag_index_b<16>(m.c0 + nb, m.r0 + kb, m.rows)) =
+            pack_bf16_column(lds, kb, nb);
     }
 }
 
@@ -1365,12 +1367,14 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         TimedLaunch tl(MG_K_ADAM, st);
         dev::AdamArgs aa;
         aa.param = pv.params;
-        aa.frag_fwd32 = pv.frag_fwd32;
-        aa.frag_fwd16 = pv.frag_fwd16;
-        aa.frag_bwd16 = pv.frag_bwd16;
-        aa.frag_fwd32_bf = pv.frag_fwd32_bf;
-        aa.frag_fwd16_bf = pv.frag_fwd16_bf;
-        aa.frag_bwd16_bf = pv.frag_bwd16_bf;
+        // only the copies the next minibatch's row pass reads; the others are
+        // derived once before the next collect or forward
+        aa.frag_fwd32 = nullptr;
+        aa.frag_fwd16 = bf ? nullptr : pv.frag_fwd16;
+        aa.frag_bwd16 = bf ? nullptr : pv.frag_bwd16;
+        aa.frag_fwd32_bf = nullptr;
+        aa.frag_fwd16_bf = bf ? pv.frag_fwd16_bf : nullptr;
+        aa.frag_bwd16_bf = bf ? pv.frag_bwd16_bf : nullptr;
         aa.grad = ws.grad;
         aa.mom = m;
         aa.var = v;

@@ -124,6 +124,46 @@ def test_collect_full_size_subset(mg, orc, env, n, block):
     check_minibatch(model, orc, d, orc.hparams(), p0, block_rows(s, n, B, block), B)
 
 
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_collect_and_forward_after_train(mg, orc, precision):
+    """train() rewrites only the weight copies its own row pass reads; collect
+    (64-row tiles here, which read the 32-wide copies) and forward() after it
+    must see the trained weights. The oracle continues from the GPU's env
+    state after the first collect and replays the second one teacher-forced
+    with the post-train parameters."""
+    bf16 = precision == "bf16"
+    close = (lambda g, w, what: assert_close_bf16(g, w, what)) if bf16 else \
+        (lambda g, w, what: assert_close(g, w, TOL_HEAD, what))
+    eid, kernel = ENVS["cartpole"]
+    n, T = 64 * 512, 2
+    gym = mg.Gym(kernel, n, 0)
+    model = mg.PPOModel(gym, horizon=T, precision=precision)
+    d = orc.dims(eid, bf16=bf16)
+    model.collect()
+    s = model.download_slots()
+    g = orc.GymState(eid, n, 0)
+    g.state[:] = gym.state()
+    g.rng[:] = gym.rng()
+    g.done[:] = gym.done()
+    slots = orc.Slots(eid, n, T)
+    slots.obs[:] = s["obs"]
+    p0 = model.params()
+    model.train(1)
+    p1 = model.params()
+    assert np.abs(p1 - p0).max() > 1e-6, "training left the weights unchanged"
+    model.collect()
+    s = model.download_slots()
+    orc.collect(g, d, p1, T, slots, first=False, teacher_actions=s["actions"], threads=THREADS)
+    assert_bit_exact(s["obs"], slots.obs, "obs slots after train")
+    close(s["value"], slots.value, "values after train")
+    close(s["logp"], slots.logp, "logp after train")
+    close(model.head(), slots.head, "bootstrap head after train")
+    model.train(1)
+    rs = np.random.default_rng(9)
+    obs = (rs.standard_normal((4096, gym.obs_dim)) * 2).astype(np.float32)
+    close(model.forward(obs), orc.forward(d, model.params(), obs, threads=THREADS), "forward after train")
+
+
 @pytest.mark.parametrize("n,T,layers,scale", [
     (1024, 4, 1, 1),
     (1024, 4, 3, 2),
