@@ -721,15 +721,25 @@ __global__ void __launch_bounds__(64 * kDwWaves) train_dw_kernel(const DwArgsT<f
     const uint32_t steps = rowsPer / kDwRows;
     // staging item it < 4: X rows xr + 16 it; it >= 4: Y rows yr + 32 (it - 4),
     // of the slab's 64 rows; buffer loads from the matrices' bases with this
-    // thread's byte offset in a VGPR and the row offset in an SGPR
-    const uint32_t xv = 4 * ((rb + xr) * bm.ldx + tm * kDwTileM + xc);
-    const uint32_t yv = 4 * ((rb + yr) * bm.ldy + tn * kDwTileN + yc);
+    // thread's byte offset in a VGPR and the row offset in an SGPR.
+    // With 8 splits, split s takes the rows of the row pass's 16-row tiles
+    // s, s + 8, s + 16, ...: the row-pass workgroups that wrote them ran on the
+    // same XCD as this split (workgroups go to the XCDs round robin), so part of
+    // the slabs still sit in that XCD's L2 (22.2 -> 21.9 us at 4096 rows);
+    // otherwise a split's rows are contiguous. Slab row q is then row
+    // 16 s + q % 16 + 128 (q / 16) of the minibatch.
+    const bool xcd = a.splits == 8;
+    const uint32_t xrow = xcd ? 16 * split + xr : rb + xr;
+    const uint32_t yrow = xcd ? 16 * split + (yr & 15) + 128 * (yr >> 4) : rb + yr;
+    const uint32_t rstep = xcd ? 8 : 1;  // minibatch rows per slab row, in 16-row groups
+    const uint32_t xv = 4 * (xrow * bm.ldx + tm * kDwTileM + xc);
+    const uint32_t yv = 4 * (yrow * bm.ldy + tn * kDwTileN + yc);
     auto load_item = [&](int set, int it, uint32_t sl) {
         const uint32_t r0 = (sl < steps ? sl : steps - 1) * kDwRows;
         if (it < 4)
-            px[set][it] = buffer_load16(bm.x, xv, 4 * (r0 + 16 * it) * bm.ldx);
+            px[set][it] = buffer_load16(bm.x, xv, 4 * rstep * (r0 + 16 * it) * bm.ldx);
         else
-            py[set][it - 4] = buffer_load16(bm.y, yv, 4 * (r0 + 32 * (it - 4)) * bm.ldy);
+            py[set][it - 4] = buffer_load16(bm.y, yv, 4 * rstep * (r0 + 32 * (it - 4)) * bm.ldy);
     };
     auto put_item = [&](int set, int buf, int it) {
         if (it < 4)
