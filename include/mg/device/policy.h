@@ -154,8 +154,8 @@ __device__ __forceinline__ f32x4 frag_load(const float* strip, int g) {
 }
 
 // Loads k-groups [g0, g0 + NG) of a fragment-tiled operand: one float4 per lane
-// and k-group.
-template <int M, int W, int NG>
+// and k-group, as buffer loads (BUF) or global loads.
+template <int M, int W, int NG, bool BUF = true>
 __device__ __forceinline__ void load_frag(BFrag<M, W, NG>& f, const FragSrc& src, int g0) {
     using S = Shape<M, W>;
 #pragma unroll
@@ -163,7 +163,8 @@ __device__ __forceinline__ void load_frag(BFrag<M, W, NG>& f, const FragSrc& src
         const float* strip = frag_strip<M, W>(src, ct);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            const f32x4 v = frag_load(strip, g0 + g);
+            const f32x4 v = BUF ? frag_load(strip, g0 + g)
+                                : *reinterpret_cast<const f32x4*>(strip + 4 * (threadIdx.x & 63) + 256 * (g0 + g));
 #pragma unroll
             for (int j = 0; j < 4; ++j) f.b[g][ct][j] = v[j];
         }
@@ -199,8 +200,9 @@ __device__ __forceinline__ void gemm_frag(AccTile<M, W>& acc, const float* a_lds
 // 64-row tiles (two workgroups per CU) whose weight operands are known in
 // advance: the two halves of the current GEMM's fragment, each refilled with
 // the next GEMM's half once consumed, so the loads' L2 latency overlaps the MFMA
-// work (and the barriers) in between instead of stalling every k-group.
-template <int M, int W = 4>
+// work (and the barriers) in between instead of stalling every k-group. BUF:
+// buffer loads (load_frag).
+template <int M, int W = 4, bool BUF = true>
 struct WStream {
     static_assert(Shape<M, W>::MT == 32, "32x32x2 tiles");
     static constexpr int NG = kEmbed / Shape<M, W>::KG / 2;  // k-groups per half
@@ -212,8 +214,8 @@ struct WStream {
     __device__ __forceinline__ void start(int n, Src src) {
         total = n;
         const FragSrc f0 = src(0);
-        load_frag<M, W, NG>(b[0], f0, 0);
-        load_frag<M, W, NG>(b[1], f0, NG);
+        load_frag<M, W, NG, BUF>(b[0], f0, 0);
+        load_frag<M, W, NG, BUF>(b[1], f0, NG);
     }
 
     // acc += A @ W_s for the s-th GEMM of the sequence, then refills the
@@ -230,9 +232,9 @@ struct WStream {
         // measurable difference since they are staged in LDS)
         __builtin_amdgcn_s_setprio(1);
         gemm_frag<M, W, NG>(acc, a_lds, b[0], 0);
-        if (more) load_frag<M, W, NG>(b[0], f, 0);
+        if (more) load_frag<M, W, NG, BUF>(b[0], f, 0);
         gemm_frag<M, W, NG>(acc, a_lds, b[1], NG);
-        if (more) load_frag<M, W, NG>(b[1], f, NG);
+        if (more) load_frag<M, W, NG, BUF>(b[1], f, NG);
         __builtin_amdgcn_s_setprio(0);
     }
 };
@@ -480,11 +482,11 @@ __device__ __forceinline__ SmallParams small_params(const mg_policy_view& pv) {
 
 // Whole forward: obs staged in obsL ([M][O], LDS) -> head in headL ([M][HD], LDS).
 // 16-row tiles stream whole fragments (TStream), taller tiles half-fragments
-// (WStream).
-template <int M, int W = 4>
+// (WStream; BUF: with buffer loads).
+template <int M, int W = 4, bool BUF = true>
 __device__ __forceinline__ void policy_forward(const mg_policy_view& pv, const SmallParams& sp, FwdSmem<M>& sm,
                                                FwdRegs<M, W>& R, const float* obsL, int O, float* headL, int HD) {
-    using Stream = typename std::conditional<M == 16, TStream<M, W>, WStream<M, W>>::type;
+    using Stream = typename std::conditional<M == 16, TStream<M, W>, WStream<M, W, BUF>>::type;
     using Seq = FwdSeq<Shape<M, W>::MT>;
     const int NC = (int)pv.hidden / kChunk;
     const Seq seq{&pv, NC};
