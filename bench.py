@@ -230,10 +230,20 @@ def profile_pass(which):
     262144-env collect and random rollout, 64 train minibatches, and one 1 GiB
     device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters
     ("all" adds 64 copies of the Adam step's byte count, its size floor).
-    "bf16": the collect and the minibatches in bf16 mode, and the copy."""
+    "bf16": the collect and the minibatches in bf16 mode, and the copy.
+    "train": one collect and two train(1) epochs of the 262144-env fp32 loop
+    (2048 minibatches each, enqueued back to back as in the benchmark)."""
     import metalgym_amd as mg
 
     n, T = 262144, 32
+    if which == "train":
+        gym = mg.Gym("rollout_cartpole", n, 0)
+        model = mg.PPOModel(gym, horizon=T)
+        model.collect()
+        for e in range(2):
+            model.train(1)
+            print(f"profile: train(1) epoch {e} of 2048 minibatches of 4096 rows", flush=True)
+        return
     if which in ("collect", "all", "bf16"):
         precision = "bf16" if which == "bf16" else "fp32"
         gym = mg.Gym("rollout_cartpole", n, 0)
@@ -281,7 +291,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--profile", choices=["collect", "random", "copy", "all", "bf16"], default=None,
+    ap.add_argument("--profile", choices=["collect", "random", "copy", "all", "bf16", "train"], default=None,
                     help="run short kernel passes for rocprofv3 instead of the benchmark")
     args = ap.parse_args()
     if args.gpus != 1:
