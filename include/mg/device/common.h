@@ -82,6 +82,18 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Sum of t[0..N) as a pairwise tree (t[c] + t[c + N/2], then halves again),
+// five dependent adds for 32 terms instead of 31; N a power of two. Overwrites t.
+template <int N>
+__device__ __forceinline__ float tree_sum(float (&t)[N]) {
+    static_assert(N >= 1 && (N & (N - 1)) == 0, "power-of-two count");
+#pragma unroll
+    for (int w = N / 2; w >= 1; w /= 2)
+#pragma unroll
+        for (int c = 0; c < w; ++c) t[c] = t[c] + t[c + w];
+    return t[0];
+}
+
 // Maximum over groups of G consecutive lanes, the same partner pattern.
 template <int G>
 __device__ __forceinline__ float group_max(float v) {

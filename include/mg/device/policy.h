@@ -329,6 +329,20 @@ __device__ __forceinline__ void fwd_embed(const float* Win, const float* bias, c
     }
 }
 
+// A thread's part of a row sum: a pairwise tree for 16 or more terms, else in
+// order (see fwd_layernorm). Overwrites t.
+template <int N>
+__device__ __forceinline__ float row_sum(float (&t)[N]) {
+    if constexpr (N >= 16) {
+        return tree_sum(t);
+    } else {
+        float s = t[0];
+#pragma unroll
+        for (int c = 1; c < N; ++c) s += t[c];
+        return s;
+    }
+}
+
 // model/layernorm.metal:10-71 on the register tile; the result goes to sm.xs.
 // If xn_out/sd_out/x_out are given, the normalised values, the standard
 // deviation and the output are also written there ([M][128], [M], [M][128],
@@ -354,18 +368,21 @@ __device__ __forceinline__ void fwd_layernorm(Smem& sm, const FwdRegs<M, W>& R, 
         f32x4 v = *reinterpret_cast<const f32x4*>(xr + c);
         x[c] = v[0], x[c + 1] = v[1], x[c + 2] = v[2], x[c + 3] = v[3];
     }
-    float s = 0.0f;
+    // a thread's sums as pairwise trees where it holds 16 or 32 columns (32-
+    // and 64-row tiles), whose 31-add chains lengthened the LN phase (the
+    // 262144-env collect 35.19 -> 34.90 ms); in column order at 4 columns (the
+    // train kernels, whose bf16 mode rounds the LN output)
+    float t[CPT];
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) s += x[c];
-    s = group_sum<TPR>(s);
+    for (int c = 0; c < CPT; ++c) t[c] = x[c];
+    const float s = group_sum<TPR>(row_sum(t));
     const float mean = s / (float)kEmbed;
-    float q = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        float d = x[c] - mean;
-        q += d * d;
+        const float d = x[c] - mean;
+        t[c] = d * d;
     }
-    q = group_sum<TPR>(q);
+    const float q = group_sum<TPR>(row_sum(t));
     const float var = q / (float)kEmbed;
     const float sd = sqrtf(var + 1e-5f);
     const float rstd = 1.0f / sd;
@@ -456,10 +473,10 @@ __device__ __forceinline__ void fwd_head(const float* Wh, Smem& sm, float* headL
         x[c] = v[0], x[c + 1] = v[1], x[c + 2] = v[2], x[c + 3] = v[3];
     }
     for (int j = 0; j < HD; ++j) {
-        float acc = 0.0f;
+        float t[CPT];
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) acc += x[c] * wp[c * HD + j];
-        acc = group_sum<TPR>(acc);
+        for (int c = 0; c < CPT; ++c) t[c] = x[c] * wp[c * HD + j];
+        const float acc = group_sum<TPR>(row_sum(t));
         if (part == 0) headL[row * HD + j] = acc;
     }
     __syncthreads();
