@@ -167,12 +167,12 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
 
     for (uint32_t t = 0; t <= T; ++t) {
         if constexpr (BF16)
-            policy_forward_b<M, CS::W>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward_b<M, CS::W, HD>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
         else
             // global weight loads when the env states sit in LDS: there the
             // buffer loads' scalar descriptors cost the heightmap env more
             // spilling than they save (VoxelNav at 262144 envs, 135 -> 151 ms)
-            policy_forward<M, CS::W, !LS::USE>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward<M, CS::W, !LS::USE, HD>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
         if (envLane) {
             const float* h = sm.head + tid * HD;
             if (t == T) {  // bootstrap head for GAE and headValue()

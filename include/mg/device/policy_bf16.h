@@ -252,8 +252,8 @@ __device__ __forceinline__ void fwd_block_b(const mg_policy_view& pv, int l, Fwd
 }
 
 // Whole forward with bf16 GEMM operands: obs staged in obsL ([M][O], LDS) ->
-// head in headL ([M][HD], LDS).
-template <int M, int W = 4>
+// head in headL ([M][HD], LDS). HDC: HD when known at compile time.
+template <int M, int W = 4, int HDC = 0>
 __device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, const SmallParams& sp, FwdSmemB<M>& sm,
                                                  FwdRegs<M, W>& R, const float* obsL, int O, float* headL, int HD) {
     using Stream = typename std::conditional<M == 16, TStreamB<M, W>, WStreamB<M, W>>::type;
@@ -270,7 +270,7 @@ __device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, const
     }
     const float* g = sp.ln + 2 * kEmbed * pv.layers;
     fwd_layernorm<M, W>(sm, R, g, g + kEmbed);
-    fwd_head<M, W>(sp.wh, sm, headL, HD);
+    fwd_head<M, W, HDC>(sp.wh, sm, headL, HD);
 }
 
 }  // namespace dev
