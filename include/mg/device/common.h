@@ -41,6 +41,13 @@ __device__ __forceinline__ f32x4 buffer_load16(const void* base, uint32_t voff, 
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
 
+// One float per lane, addressed as buffer_load16.
+__device__ __forceinline__ float buffer_load4(const void* base, uint32_t voff, uint32_t soff) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
 __device__ __forceinline__ int c32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 __device__ __forceinline__ int c16_row(int r, int lane) { return 4 * (lane >> 4) + r; }
 

@@ -1,5 +1,5 @@
-// One PPO minibatch update (model/ppo.h:906-916) as four launches (three in
-// bf16 mode at the usual shapes, where 2 and 3 are one kernel):
+// One PPO minibatch update (model/ppo.h:906-916) as four launches (three at
+// the usual shapes, where 2 and 3 are one kernel):
 //
 //  1. train_rows: per 16-row tile (256 workgroups for 4096 rows), the forward
 //     recompute with activation capture (model/ppo.h:909), the loss and head
@@ -8,15 +8,17 @@
 //     activations and gradients the weight gradients need.
 //     The same workgroup writes its tile's sums of the vector-parameter, head
 //     and log_std gradients and of the loss statistics.
-//  2. train_dw: the block matrices' gradients X^T dY as 64x64 MFMA tiles,
-//     the rows split into ranges (fp32: LDS-staged slabs; bf16: operands
-//     loaded straight into registers from row-group-packed captures).
+//  2. train_dw: the block matrices' gradients X^T dY as MFMA tiles, the rows
+//     split into ranges (fp32: 128x64 tiles from LDS-staged slabs; bf16: 64x64
+//     tiles, operands loaded straight into registers from row-group-packed
+//     captures).
 //  3. grad_reduce: sums the tile partials and the row splits in fixed order,
 //     writes the minibatch's LossStats (model/ppo.h:925-943) and one partial
 //     squared norm per workgroup.
-//     (bf16 with 128 to 1024 tiles of 32 x 32: train_dw_bf16_fused computes
-//     the weight gradients without row splits and does this step's tile sums
-//     and partial norms in the same launch.)
+//     (With 128 to 1024 tiles of 32 x 32: train_dw_fused, or
+//     train_dw_bf16_fused in bf16 mode, computes the weight gradients without
+//     row splits and does this step's tile sums and partial norms in the same
+//     launch.)
 //  4. adam: every workgroup adds the partial norms in the same fixed order
 //     (so no cross-workgroup synchronisation is needed), applies the clip
 //     scale and Adam (model/optimizer.metal:23-60).
@@ -912,12 +914,13 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
 // The kernel moves ≈50 MB between L2 and the fabric, more than the 20 MB of
 // captures: each XCD fetches the capture blocks its tiles share. Against the
 // split kernel plus grad_reduce it saves one launch per minibatch.)
+template <class T>
 struct DwFusedArgs {
-    DwArgsT<uint16_t> dw;
+    DwArgsT<T> dw;
     ReduceArgs red;
 };
 template <int NW, int U>
-__global__ void __launch_bounds__(64 * NW) train_dw_bf16_fused_kernel(const DwFusedArgs a) {
+__global__ void __launch_bounds__(64 * NW) train_dw_bf16_fused_kernel(const DwFusedArgs<uint16_t> a) {
     __shared__ float red[NW][32 * 32];
     float sq = 0.0f;
     {
@@ -980,6 +983,82 @@ __global__ void __launch_bounds__(64 * NW) train_dw_bf16_fused_kernel(const DwFu
         for (uint32_t i = gridDim.x + threadIdx.x; i < (uint32_t)kReduceBlocks; i += 64 * NW) a.red.normpart[i] = 0.0f;
 }
 constexpr int kDwfWaves = 8;
+
+// The fp32 counterpart of train_dw_bf16_fused_kernel, reading the row-major
+// captures directly: lane (i = l % 32, k = l / 32) of a
+// v_mfma_f32_32x32x2_f32 over rows r, r + 1 takes X[r + k][i] and Y[r + k][i]
+// of its tile's columns as dword buffer loads (a half-wave reads one row's 128
+// contiguous bytes), the row offset in an SGPR. Wave w takes the row pairs
+// 2 (NW s + w), s = 0, 1, ..., in batches of U pairs loaded NB - 1 batches
+// ahead into a ring of NB register sets (no copies between sets, so each
+// MFMA waits only for its own two loads; batches past the end reload the
+// last one), and the NW wave tiles are added in LDS in wave order. (A probe on the MI355X with two waves per SIMD: two dword loads per
+// MFMA cost 8.6% of the MFMA rate, two 16-byte loads per four MFMAs 14%.)
+// Workgroup b runs on XCD b % 8 and takes tile (b % 8) (T / 8) + b / 8 of
+// the T tiles, ordered (matrix, hidden block, embed block): an XCD's tiles
+// are all embed columns of a run of hidden blocks of one matrix, so each
+// capture column strip is fetched into as few L2s as can be. Then the
+// tile-partial columns and the norm part as in train_dw_bf16_fused_kernel.
+template <int NW, int U, int NB>
+__global__ void __launch_bounds__(64 * NW) train_dw_fused_kernel(const DwFusedArgs<float> a) {
+    __shared__ float red[NW][32 * 32];
+    float sq = 0.0f;
+    {
+        const uint32_t per = a.dw.tiles_per_big[0];  // every matrix has E H / 1024 tiles
+        const uint32_t t = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+        const uint32_t mi = t / per, eb = (t % per) % (kEmbed / 32), hb = (t % per) / (kEmbed / 32);
+        const BigMatT<float>& bm = a.dw.big[mi];
+        const bool up = bm.mdim == (uint32_t)kEmbed;  // up: X is the embed side
+        const uint32_t tm = up ? eb : hb, tn = up ? hb : eb;
+        const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+        const uint32_t xv = 4 * ((lane >> 5) * bm.ldx + tm * 32 + (lane & 31));
+        const uint32_t yv = 4 * ((lane >> 5) * bm.ldy + tn * 32 + (lane & 31));
+        const uint32_t batches = a.dw.rows / (2 * NW * U);  // rows: a multiple of 2 NW U NB
+        auto load = [&](float (&op)[U][2], uint32_t b) {
+            b = b < batches ? b : batches - 1;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t r = 2 * (NW * (b * U + u) + w);
+                op[u][0] = buffer_load4(bm.x, xv, 4 * r * bm.ldx);
+                op[u][1] = buffer_load4(bm.y, yv, 4 * r * bm.ldy);
+            }
+        };
+        f32x16 acc = f32x16{};
+        float op[NB][U][2];
+#pragma unroll
+        for (int i = 0; i + 1 < NB; ++i) {
+            load(op[i], i);
+            __builtin_amdgcn_sched_barrier(0);  // batch 0 first, so its MFMAs wait for it alone
+        }
+        for (uint32_t b = 0; b < batches; b += NB) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                // kept in this order: the loads, then the batch's MFMAs
+                load(op[(i + NB - 1) % NB], b + i + NB - 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc = mfma32x32x2(op[i][u][0], op[i][u][1], acc);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[w][c32_row(r, lane) * 32 + (lane & 31)] = acc[r];
+        __syncthreads();
+        float* out = a.red.grad + bm.off + (size_t)tm * 32 * bm.ndim + tn * 32;
+        for (int e = threadIdx.x; e < 32 * 32; e += 64 * NW) {
+            float v = red[0][e];
+#pragma unroll
+            for (int q = 1; q < NW; ++q) v += red[q][e];
+            out[(size_t)(e >> 5) * bm.ndim + (e & 31)] = v;
+            sq += v * v;
+        }
+    }
+    sq += reduce_tile_partials<64 * NW>(a.red, blockIdx.x, gridDim.x);
+    write_norm_part<NW>(sq, a.red.normpart + blockIdx.x);
+    if (blockIdx.x == 0)
+        for (uint32_t i = gridDim.x + threadIdx.x; i < (uint32_t)kReduceBlocks; i += 64 * NW) a.red.normpart[i] = 0.0f;
+}
+constexpr int kDwf32Waves = 8, kDwf32U = 8, kDwf32Sets = 2;
 
 // The block matrices are contiguous from float_group: per block up [128 x H]
 // then down [H x 128]. Both matrix kinds split into (128 x H) / 1024 tiles of
@@ -1355,16 +1434,26 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
     // kRedCols tile-partial columns per small workgroup, at most half the grid
     const uint32_t cols = pv.float_group + E * pv.head_dim + 5, cw = dev::kRedCols;
     ga.small_wgs = (cols + cw - 1) / cw < kReduceBlocks / 2 ? (cols + cw - 1) / cw : kReduceBlocks / 2;
-    // bf16 with 128 to 1024 tiles of 32 x 32: weight gradients without row
-    // splits, fused with the tile-partial sums (one launch instead of two)
+    // 128 to 1024 tiles of 32 x 32: weight gradients without row splits,
+    // fused with the tile-partial sums (one launch instead of two; fp32 at
+    // 4096 rows, 2 blocks, hidden 512: 71.8 -> 67.9 us per minibatch)
     const uint32_t tiles32 = 2 * L * (E / 32) * (H / 32);
     if (bf && tiles32 >= 128 && tiles32 <= (uint32_t)kReduceBlocks && B % (16 * dev::kDwfWaves) == 0) {
         TimedLaunch tl(MG_K_TRAIN_DW, st);
-        dev::DwFusedArgs fa;
+        dev::DwFusedArgs<uint16_t> fa;
         fa.dw = dw_args<uint16_t>(pv, ws, B, 1, 32);
         fa.red = ga;
         hipLaunchKernelGGL((dev::train_dw_bf16_fused_kernel<dev::kDwfWaves, 4>), dim3(tiles32),
                            dim3(64 * dev::kDwfWaves), 0, st, fa);
+        MG_HIP(hipGetLastError(), "train dW launch");
+    } else if (!bf && tiles32 >= 128 && tiles32 <= (uint32_t)kReduceBlocks &&
+               B % (2 * dev::kDwf32Waves * dev::kDwf32U * dev::kDwf32Sets) == 0) {
+        TimedLaunch tl(MG_K_TRAIN_DW, st);
+        dev::DwFusedArgs<float> fa;
+        fa.dw = dw_args<float>(pv, ws, B, 1, 32);
+        fa.red = ga;
+        hipLaunchKernelGGL((dev::train_dw_fused_kernel<dev::kDwf32Waves, dev::kDwf32U, dev::kDwf32Sets>), dim3(tiles32),
+                           dim3(64 * dev::kDwf32Waves), 0, st, fa);
         MG_HIP(hipGetLastError(), "train dW launch");
     } else {
         {  // 2. block-matrix weight gradients
