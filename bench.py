@@ -123,7 +123,7 @@ def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32"):
                                   [round(x, 6) for x in st.as_tuple()]))}
     kern = {}
     for k in ("collect", "gae", "adv_stats", "train_rows", "train_dw", "grad_reduce", "adam"):
-        if times[k][1]:  # bf16 at the default shape fuses grad_reduce into train_dw
+        if times[k][1]:  # at the default shape grad_reduce is fused into train_dw
             kern[k + "_us"] = round(kernel_avg_ms(times, k) * 1e3, 2)
     tr = kernel_avg_ms(times, "train_rows") * 1e-3
     dw = kernel_avg_ms(times, "train_dw") * 1e-3
