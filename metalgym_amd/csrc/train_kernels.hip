@@ -992,13 +992,16 @@ constexpr int kDwfWaves = 8;
 // 2 (NW s + w), s = 0, 1, ..., in batches of U pairs loaded NB - 1 batches
 // ahead into a ring of NB register sets (no copies between sets, so each
 // MFMA waits only for its own two loads; batches past the end reload the
-// last one), and the NW wave tiles are added in LDS in wave order. (A probe on the MI355X with two waves per SIMD: two dword loads per
-// MFMA cost 8.6% of the MFMA rate, two 16-byte loads per four MFMAs 14%.)
-// Workgroup b runs on XCD b % 8 and takes tile (b % 8) (T / 8) + b / 8 of
-// the T tiles, ordered (matrix, hidden block, embed block): an XCD's tiles
-// are all embed columns of a run of hidden blocks of one matrix, so each
-// capture column strip is fetched into as few L2s as can be. Then the
-// tile-partial columns and the norm part as in train_dw_bf16_fused_kernel.
+// last one), and the NW wave tiles are added in LDS in wave order. (A probe
+// on the MI355X with two waves per SIMD: two dword loads per MFMA cost 8.6%
+// of the MFMA rate, two 16-byte loads per four MFMAs 14%.) Workgroup b runs
+// on XCD b % 8 and takes tile (b % 8) (T / 8) + b / 8 of the T tiles, ordered
+// (matrix, hidden block, embed block): an XCD's tiles are all embed columns
+// of a run of hidden blocks of one matrix, so each capture column strip is
+// fetched into as few L2s as can be (4096 rows, 2 blocks, hidden 512: 19.6 us
+// against 26.7 us with tile b on workgroup b). The loop is bound by each CU's
+// 1 MB of capture reads through L1 misses. Then the tile-partial columns and
+// the norm part as in train_dw_bf16_fused_kernel.
 template <int NW, int U, int NB>
 __global__ void __launch_bounds__(64 * NW) train_dw_fused_kernel(const DwFusedArgs<float> a) {
     __shared__ float red[NW][32 * 32];
