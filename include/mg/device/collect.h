@@ -89,6 +89,9 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
     using CS = CollectShape<M, Env::OBS_DIM>;
     using LS = LdsState<Env, M, BF16>;
     constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
+    // parts of a split observation per env, spread over the whole workgroup
+    // when the states sit in LDS (0: the env lanes call step())
+    constexpr uint32_t KS = LS::USE ? Tr::OBS_SPLIT : 0;
     __shared__ CollectSmem<M, O, HD, BF16> sm;
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     using SS = SmallStage<Env, M, BF16>;
@@ -192,15 +195,38 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
                 if (done) Env::reset(S(), rng);
                 Obs o{};
                 float r = 0.0f;
-                Env::step(S(), act, o, r, done);
                 const float* of = reinterpret_cast<const float*>(&o);
+                if constexpr (KS > 0) {  // the floats from KS on; the parts after the barrier below
+                    Env::stepState(S(), act, r, done);
+                    Env::observeRest(S(), o);
 #pragma unroll
-                for (int q = 0; q < O; ++q) obs[q] = of[q];
-                store_floats<O>(a.obs_slots + (k + n) * O, obs);
+                    for (int q = KS; q < O; ++q) {
+                        a.obs_slots[(k + n) * O + q] = of[q];
+                        sm.obs[tid * O + q] = of[q];
+                    }
+                } else {
+                    Env::step(S(), act, o, r, done);
+#pragma unroll
+                    for (int q = 0; q < O; ++q) obs[q] = of[q];
+                    store_floats<O>(a.obs_slots + (k + n) * O, obs);
+#pragma unroll
+                    for (int q = 0; q < O; ++q) sm.obs[tid * O + q] = obs[q];
+                }
                 a.reward_slots[k] = r;
                 a.done_slots[k] = done;
-#pragma unroll
-                for (int q = 0; q < O; ++q) sm.obs[tid * O + q] = obs[q];
+            }
+        }
+        if constexpr (KS > 0) {
+            if (t < T) {
+                __syncthreads();  // every env lane's state is stepped
+                // part p of env e, consecutive threads on consecutive parts
+                const size_t row0 = ((size_t)(t + 1) * n + (size_t)blockIdx.x * M) * O;
+                for (uint32_t q = tid; q < M * KS; q += CS::NT) {
+                    const uint32_t e = q / KS, p = q % KS;
+                    const float v = Env::observePart(*reinterpret_cast<const State*>(lds_state + e * LS::STRIDE), p);
+                    sm.obs[e * O + p] = v;
+                    a.obs_slots[row0 + (size_t)e * O + p] = v;
+                }
             }
         }
         __syncthreads();

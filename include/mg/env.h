@@ -14,6 +14,20 @@
 //       MG_HD static void step(State& s, Action a, Obs& obs, float& reward, uint8_t& done);
 //   };
 //
+// Optional split observation, for an observation made of independent parts
+// (e.g. ray casts): an env that also defines
+//
+//       static constexpr uint32_t OBS_SPLIT = K;   // the first K floats of Obs
+//       MG_HD static void stepState(State& s, Action a, float& reward, uint8_t& done);
+//       MG_HD static float observePart(const State& s, uint32_t k);   // Obs float k < K
+//       MG_HD static void observeRest(const State& s, Obs& obs);      // the floats >= K
+//
+// promises that step(s, a, obs, r, d) is stepState(s, a, r, d) followed by
+// obs float k = observePart(s, k) for every k < K and observeRest(s, obs),
+// with the same results. Kernels that hold a tile's states where all of its
+// threads can read them (collect with the states staged in LDS) then spread
+// the tile's K parts per env over all the threads; the others call step().
+//
 // This mirrors the reference's Env template (README.md:21-66; rollout.h:31-54):
 // same member names, same reset/step contract, one struct instead of a Metal
 // twin plus a host twin. A .hip file that includes <mg/device/env_kernels.h> and
@@ -56,6 +70,15 @@ MG_HD uint32_t env_seed(uint32_t seed, uint32_t i) {
     return s ? s : 0x6D2B79F5u;
 }
 
+template <typename Env, typename = void>
+struct ObsSplit {
+    static constexpr uint32_t value = 0;
+};
+template <typename Env>
+struct ObsSplit<Env, std::void_t<decltype(Env::OBS_SPLIT)>> {
+    static constexpr uint32_t value = Env::OBS_SPLIT;
+};
+
 template <typename Env>
 struct EnvTraits {
     using State = typename Env::State;
@@ -73,6 +96,9 @@ struct EnvTraits {
     static_assert(!CONTINUOUS || sizeof(Action) == ACT_DIM * sizeof(float),
                   "the Gaussian head needs an Action of exactly ACT_DIM floats");
     static_assert(ACT_DIM >= 1 && ACT_DIM + 1 <= 64, "ACT_DIM + value must fit a 64-wide head");
+    // the optional split observation's part count (0: none)
+    static constexpr uint32_t OBS_SPLIT = ObsSplit<Env>::value;
+    static_assert(OBS_SPLIT <= OBS_DIM, "OBS_SPLIT counts floats of Obs");
 };
 
 }  // namespace mg

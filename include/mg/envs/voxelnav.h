@@ -105,33 +105,46 @@ struct VoxelNav {
         s.cobble = START_COBBLE;
     }
 
-    MG_HD static void observe(const State& s, Obs& o) {
+    // Depth of the ray of pitch row r from eye height ey along yaw direction
+    // (ca, sa): the first 0.5-cell sample off the grid or at or below a column
+    // top, else MAX_DEPTH; divided by MAX_DEPTH.
+    MG_HD static float march(const State& s, float ey, float ca, float sa, uint32_t r) {
         const float pitches[RAY_ROWS] = {-45.0f, -20.0f, 0.0f, 15.0f};
-        const float h = heightAt(s, s.x, s.z);
-        const float ey = h + EYE;
-        for (uint32_t c = 0; c < RAY_COLS; c++) {
-            const float a = s.yaw + ((float)c / (float)(RAY_COLS - 1) - 0.5f) * FOV;
-            const float ca = mg::cosf(a), sa = mg::sinf(a);
-            for (uint32_t r = 0; r < RAY_ROWS; r++) {
-                const float p = pitches[r] * PI / 180.0f;
-                const float cp = mg::cosf(p);
-                const float dx = cp * ca, dy = mg::sinf(p), dz = cp * sa;
-                float depth = MAX_DEPTH;
-                for (float t = 0.5f; t < MAX_DEPTH; t += 0.5f) {
-                    const float px = s.x + t * dx, py = ey + t * dy, pz = s.z + t * dz;
-                    const int cx = (int)floorf(px), cz = (int)floorf(pz);
-                    if (!inside(cx, cz)) {
-                        depth = t;
-                        break;
-                    }
-                    if (py <= (float)s.height[cell(cx, cz)]) {
-                        depth = t;
-                        break;
-                    }
-                }
-                o.ray[c * RAY_ROWS + r] = depth / MAX_DEPTH;
+        const float p = pitches[r] * PI / 180.0f;
+        const float cp = mg::cosf(p);
+        const float dx = cp * ca, dy = mg::sinf(p), dz = cp * sa;
+        float depth = MAX_DEPTH;
+        for (float t = 0.5f; t < MAX_DEPTH; t += 0.5f) {
+            const float px = s.x + t * dx, py = ey + t * dy, pz = s.z + t * dz;
+            const int cx = (int)floorf(px), cz = (int)floorf(pz);
+            if (!inside(cx, cz)) {
+                depth = t;
+                break;
+            }
+            if (py <= (float)s.height[cell(cx, cz)]) {
+                depth = t;
+                break;
             }
         }
+        return depth / MAX_DEPTH;
+    }
+    // Yaw of ray column c.
+    MG_HD static float rayYaw(const State& s, uint32_t c) {
+        return s.yaw + ((float)c / (float)(RAY_COLS - 1) - 0.5f) * FOV;
+    }
+
+    // The observation's first N_RAYS floats are independent depth samples, so
+    // kernels that hold a tile's states where all its threads can read them
+    // may compute them in parallel (observePart), then the rest (observeRest);
+    // observe() gives the same floats.
+    static constexpr uint32_t OBS_SPLIT = N_RAYS;
+    MG_HD static float observePart(const State& s, uint32_t k) {
+        const uint32_t c = k / RAY_ROWS, r = k % RAY_ROWS;
+        const float a = rayYaw(s, c);
+        return march(s, heightAt(s, s.x, s.z) + EYE, mg::cosf(a), mg::sinf(a), r);
+    }
+    MG_HD static void observeRest(const State& s, Obs& o) {
+        const float h = heightAt(s, s.x, s.z);
         const float gx = s.gx - s.x, gz = s.gz - s.z;
         const float ca = mg::cosf(s.yaw), sa = mg::sinf(s.yaw);
         o.goalForward = (gx * ca + gz * sa) / (float)W;
@@ -142,6 +155,16 @@ struct VoxelNav {
         o.cosYaw = ca;
         o.cobble = (float)s.cobble / (float)START_COBBLE;
         o.height = h / 16.0f;
+    }
+
+    MG_HD static void observe(const State& s, Obs& o) {
+        const float ey = heightAt(s, s.x, s.z) + EYE;
+        for (uint32_t c = 0; c < RAY_COLS; c++) {
+            const float a = rayYaw(s, c);
+            const float ca = mg::cosf(a), sa = mg::sinf(a);
+            for (uint32_t r = 0; r < RAY_ROWS; r++) o.ray[c * RAY_ROWS + r] = march(s, ey, ca, sa, r);
+        }
+        observeRest(s, o);
     }
 
     // A move to (nx, nz): refused off the grid or onto a column more than one
@@ -163,7 +186,8 @@ struct VoxelNav {
         return false;
     }
 
-    MG_HD static void step(State& s, Action action, Obs& obs, float& reward, uint8_t& done) {
+    // step() without its observation (the split-observation path).
+    MG_HD static void stepState(State& s, Action action, float& reward, uint8_t& done) {
         const float ca = mg::cosf(s.yaw), sa = mg::sinf(s.yaw);
         bool fell = false;
         switch (action) {
@@ -201,6 +225,10 @@ struct VoxelNav {
         if (success) reward += 10.0f;
         if (fell) reward -= 5.0f;
         done = (success || fell || s.steps >= MAX_STEPS) ? 1 : 0;
+    }
+
+    MG_HD static void step(State& s, Action action, Obs& obs, float& reward, uint8_t& done) {
+        stepState(s, action, reward, done);
         observe(s, obs);
     }
 };
