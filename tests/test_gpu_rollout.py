@@ -39,6 +39,32 @@ def test_random_rollout_bit_exact(mg, orc, env, n, steps, seed):
     assert dn.any(), "no episode ended: the test does not exercise resets"
 
 
+@pytest.mark.parametrize("n,steps,reps,seed", [
+    (4100, 40, 7, 4),     # 8 envs per workgroup, the last workgroup partial
+    (33000, 20, 13, 5),   # 16 envs per workgroup, the last workgroup partial
+])
+def test_split_rollout_sizes_bit_exact(mg, orc, n, steps, reps, seed):
+    """VoxelNav's split-observation rollout (its ray casts spread over each
+    workgroup) at the env counts that give 8 and 16 envs per workgroup, run past
+    the 250-step cap so that every env resets at least once."""
+    eid, kernel = ENVS["voxelnav"]
+    gym = mg.Gym(kernel, n, seed)
+    g = orc.GymState(eid, n, seed)
+    bufs = None
+    ended = np.zeros(n, bool)
+    for rep in range(reps):
+        bufs = gym.rollout_random(steps, bufs)
+        acts, obs, rew, dn = gym.download_slots(bufs, steps)
+        oa, oo, orw, od = orc.rollout(g, steps, random=True, threads=THREADS)
+        assert_bit_exact(acts, oa, f"rep {rep} actions")
+        assert_bit_exact(obs, oo, f"rep {rep} obs")
+        assert_bit_exact(rew, orw, f"rep {rep} reward")
+        assert_bit_exact(dn, od, f"rep {rep} done slots")
+        ended |= dn.any(axis=0).astype(bool)
+    compare_gym(gym, g, "end")
+    assert ended.all(), f"{int((~ended).sum())} envs never ended"
+
+
 @pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "voxelnav16", "voxelnav"])
 def test_given_action_rollout_bit_exact(mg, orc, env):
     eid, kernel = ENVS[env]
