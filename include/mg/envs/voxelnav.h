@@ -106,27 +106,31 @@ struct VoxelNav {
     }
 
     // Depth of the ray of pitch row r from eye height ey along yaw direction
-    // (ca, sa): the first 0.5-cell sample off the grid or at or below a column
-    // top, else MAX_DEPTH; divided by MAX_DEPTH.
+    // (ca, sa): the first sample t = 0.5, 1, ..., 23.5 off the grid or at or
+    // below a column top, else MAX_DEPTH; divided by MAX_DEPTH. The samples go
+    // four at a time: the four column heights are read before any is tested,
+    // so their memory latencies overlap, and the first hit in sample order
+    // wins, as in a sample-by-sample march (t = 0.5 k is exact).
     MG_HD static float march(const State& s, float ey, float ca, float sa, uint32_t r) {
         const float pitches[RAY_ROWS] = {-45.0f, -20.0f, 0.0f, 15.0f};
         const float p = pitches[r] * PI / 180.0f;
         const float cp = mg::cosf(p);
         const float dx = cp * ca, dy = mg::sinf(p), dz = cp * sa;
-        float depth = MAX_DEPTH;
-        for (float t = 0.5f; t < MAX_DEPTH; t += 0.5f) {
-            const float px = s.x + t * dx, py = ey + t * dy, pz = s.z + t * dz;
-            const int cx = (int)floorf(px), cz = (int)floorf(pz);
-            if (!inside(cx, cz)) {
-                depth = t;
-                break;
+        constexpr uint32_t kSamples = 47;  // t = 0.5 k < MAX_DEPTH
+        for (uint32_t k0 = 1; k0 <= kSamples; k0 += 4) {
+            bool hit[4];
+            for (uint32_t u = 0; u < 4; u++) {
+                const float t = 0.5f * (float)(k0 + u);
+                const float px = s.x + t * dx, py = ey + t * dy, pz = s.z + t * dz;
+                const int cx = (int)floorf(px), cz = (int)floorf(pz);
+                const bool in = inside(cx, cz);
+                const float top = (float)s.height[in ? cell(cx, cz) : 0u];
+                hit[u] = k0 + u <= kSamples && (!in || py <= top);
             }
-            if (py <= (float)s.height[cell(cx, cz)]) {
-                depth = t;
-                break;
-            }
+            for (uint32_t u = 0; u < 4; u++)
+                if (hit[u]) return 0.5f * (float)(k0 + u) / MAX_DEPTH;
         }
-        return depth / MAX_DEPTH;
+        return MAX_DEPTH / MAX_DEPTH;
     }
     // Yaw of ray column c.
     MG_HD static float rayYaw(const State& s, uint32_t c) {
