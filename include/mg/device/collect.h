@@ -21,15 +21,18 @@ namespace dev {
 
 // Launch shape per tile height: 64- and 32-row tiles run 4 waves and two
 // workgroups per CU (one when the env lane holds more than 32 observation
-// floats, which do not fit beside the weights at two); 16-row tiles (runs of
-// at most 512 workgroups, one per CU) of envs with up to 16 observation floats
-// run 8 waves, 16 output columns each (a wider observation held by the env
-// lane would not fit the register budget of 8 waves).
-template <int M, int O>
+// floats, which do not fit beside the weights at two, unless WIDE); 16-row
+// tiles (runs of at most 512 workgroups, one per CU) of envs with up to 16
+// observation floats run 8 waves, 16 output columns each (a wider observation
+// held by the env lane would not fit the register budget of 8 waves).
+// WIDE: an env with a split observation whose states stay in device memory,
+// two workgroups per CU (VoxelNav's 40 observation floats: 231 VGPRs, no
+// spills), so one workgroup's env phase overlaps the other's GEMMs.
+template <int M, int O, bool WIDE = false>
 struct CollectShape {
     static constexpr int W = M == 16 && O <= 16 ? 8 : 4;
     static constexpr int NT = 64 * W;
-    static constexpr int MIN_WG = M == 16 || O > 32 ? 1 : 2;  // workgroups per CU
+    static constexpr int MIN_WG = M == 16 || (O > 32 && !WIDE) ? 1 : 2;  // workgroups per CU
 };
 
 template <int M, int O, int HD, bool BF16>
@@ -45,7 +48,7 @@ struct CollectSmem {
 // forward's LDS at the kernel's workgroups per CU; gathers from a state (a
 // VoxelNav heightmap's ray march) then cost an LDS round trip instead of a
 // cache miss.
-template <typename Env, int M, bool BF16>
+template <typename Env, int M, bool BF16, bool WIDE = false>
 struct LdsState {
     using State = typename Env::State;
     static constexpr uint32_t SD = sizeof(State) / 4;           // dwords per state
@@ -54,7 +57,7 @@ struct LdsState {
     static constexpr int O = Env::OBS_DIM, HD = Env::ACT_DIM + 1;
     // 256 bytes of headroom for the compiler's alignment padding between the
     // two static LDS arrays
-    static constexpr bool USE = !EnvTraits<Env>::STATE_IN_REGISTERS && sizeof(State) % 4 == 0 &&
+    static constexpr bool USE = !WIDE && !EnvTraits<Env>::STATE_IN_REGISTERS && sizeof(State) % 4 == 0 &&
                                 alignof(State) <= 4 &&
                                 sizeof(CollectSmem<M, O, HD, BF16>) + BYTES + 256 <=
                                     (size_t)163840 / CollectShape<M, O>::MIN_WG;
@@ -79,19 +82,21 @@ struct SmallStage {
 };
 
 // BF16: the policy forward multiplies bfloat16 operands (policy_bf16.h).
-template <typename Env, int M, bool BF16>
-__global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectShape<M, Env::OBS_DIM>::MIN_WG))
+template <typename Env, int M, bool BF16, bool WIDE>
+__global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
+                                  (CollectShape<M, Env::OBS_DIM, WIDE>::MIN_WG))
     collect_kernel(const mg_collect_args a, const uint32_t stage_small) {
     using Tr = EnvTraits<Env>;
     using State = typename Env::State;
     using Action = typename Env::Action;
     using Obs = typename Env::Obs;
-    using CS = CollectShape<M, Env::OBS_DIM>;
-    using LS = LdsState<Env, M, BF16>;
+    using CS = CollectShape<M, Env::OBS_DIM, WIDE>;
+    using LS = LdsState<Env, M, BF16, WIDE>;
     constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
     // parts of a split observation per env, spread over the whole workgroup
-    // when the states sit in LDS (0: the env lanes call step())
-    constexpr uint32_t KS = LS::USE ? Tr::OBS_SPLIT : 0;
+    // when the states sit in LDS or (WIDE) in device memory (0: the env lanes
+    // call step())
+    constexpr uint32_t KS = LS::USE || WIDE ? Tr::OBS_SPLIT : 0;
     __shared__ CollectSmem<M, O, HD, BF16> sm;
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     using SS = SmallStage<Env, M, BF16>;
@@ -223,7 +228,9 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
                 const size_t row0 = ((size_t)(t + 1) * n + (size_t)blockIdx.x * M) * O;
                 for (uint32_t q = tid; q < M * KS; q += CS::NT) {
                     const uint32_t e = q / KS, p = q % KS;
-                    const float v = Env::observePart(*reinterpret_cast<const State*>(lds_state + e * LS::STRIDE), p);
+                    const State& se = LS::USE ? *reinterpret_cast<const State*>(lds_state + e * LS::STRIDE)
+                                              : states[(size_t)blockIdx.x * M + e];
+                    const float v = Env::observePart(se, p);
                     sm.obs[e * O + p] = v;
                     a.obs_slots[row0 + (size_t)e * O + p] = v;
                 }
@@ -244,11 +251,12 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM>::NT), (CollectS
 
 // The kernel's static LDS as the compiler laid it out (SIZE_MAX if the
 // runtime cannot tell, which turns the small-parameter staging off).
-template <typename Env, int M, bool BF16>
+template <typename Env, int M, bool BF16, bool WIDE>
 size_t collect_static_lds() {
     static const size_t bytes = [] {
         hipFuncAttributes attr{};
-        if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&collect_kernel<Env, M, BF16>)) != hipSuccess) {
+        if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&collect_kernel<Env, M, BF16, WIDE>)) !=
+            hipSuccess) {
             (void)hipGetLastError();  // not this launch's error
             return (size_t)SIZE_MAX;
         }
@@ -257,15 +265,30 @@ size_t collect_static_lds() {
     return bytes;
 }
 
-template <typename Env, int M, bool BF16>
-void launch_collect_m(const mg_collect_args* a, hipStream_t st) {
+template <typename Env, int M, bool BF16, bool WIDE>
+void launch_collect_mw(const mg_collect_args* a, hipStream_t st) {
     using SS = SmallStage<Env, M, BF16>;
-    constexpr size_t kPerWg = (size_t)163840 / CollectShape<M, Env::OBS_DIM>::MIN_WG;  // LDS per workgroup
-    const size_t stat = collect_static_lds<Env, M, BF16>();
+    constexpr size_t kPerWg = (size_t)163840 / CollectShape<M, Env::OBS_DIM, WIDE>::MIN_WG;  // LDS per workgroup
+    const size_t stat = collect_static_lds<Env, M, BF16, WIDE>();
     const size_t dyn = (size_t)SS::floats(a->policy.layers) * 4;
     const bool stage = stat <= kPerWg && dyn <= kPerWg - stat;
-    const dim3 grid(a->n / M), block(CollectShape<M, Env::OBS_DIM>::NT);
-    hipLaunchKernelGGL((collect_kernel<Env, M, BF16>), grid, block, stage ? dyn : 0, st, *a, stage ? 1u : 0u);
+    const dim3 grid(a->n / M), block(CollectShape<M, Env::OBS_DIM, WIDE>::NT);
+    hipLaunchKernelGGL((collect_kernel<Env, M, BF16, WIDE>), grid, block, stage ? dyn : 0, st, *a, stage ? 1u : 0u);
+}
+
+// An env with a split observation runs WIDE where the grid has at least two
+// workgroups per CU (VoxelNav, ms per collect of 32 steps, WIDE against its
+// states in LDS at one workgroup per CU: 70.9 / 77.9 at 262144 envs, 4.53 /
+// 5.47 at 16384; at 8192 envs, 256 workgroups, 3.23 / 2.81).
+template <typename Env, int M, bool BF16>
+void launch_collect_m(const mg_collect_args* a, hipStream_t st) {
+    if constexpr (EnvTraits<Env>::OBS_SPLIT > 0 && M >= 32) {
+        if (a->n / M >= 512) {
+            launch_collect_mw<Env, M, BF16, true>(a, st);
+            return;
+        }
+    }
+    launch_collect_mw<Env, M, BF16, false>(a, st);
 }
 
 template <typename Env, bool BF16>

@@ -61,8 +61,9 @@ def run_collect_parity(mg, orc, env, n, T, layers=2, scale=4, seed=0, collects=2
     ("cartpole_continuous_clamp", 2048, 8),
     ("voxelnav16", 1024, 8),
     ("voxelnav", 1024, 8),       # heightmaps staged in LDS: 16-row tiles
-    ("voxelnav", 8192, 2),       # 32-row tiles
-    ("voxelnav", 32768, 2),      # 64-row tiles
+    ("voxelnav", 8192, 2),       # 32-row tiles, heightmaps in LDS (256 workgroups)
+    ("voxelnav", 16384, 2),      # 32-row tiles, heightmaps in device memory, two workgroups per CU
+    ("voxelnav", 32768, 2),      # 64-row tiles, the same
 ])
 def test_collect_teacher_forced(mg, orc, env, n, T):
     run_collect_parity(mg, orc, env, n, T)
