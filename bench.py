@@ -327,7 +327,7 @@ def main():
         "data": "synthetic (seeded envs and weights)",
         "config": {"workload": "cartpole_collect_with_policy", "envs": n, "horizon": T, "embed": E, "hidden": H,
                    "layers": L, "head": "softmax(2)+value", "parallelism": "single-gpu"},
-        "roofline": {"bound": "mfma", "kernel": "collect_kernel<CartPole,64,false>", "achieved": achieved / 1e12,
+        "roofline": {"bound": "mfma", "kernel": "collect_kernel<CartPole,64,false,false>", "achieved": achieved / 1e12,
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
                      "traffic": pmc_traffic(), "flop_per_launch": flop_launch, "kernel_ms": kms},
         "gae": {"kernel_us": gae_ms * 1e3, "hbm_GBps": (n * T * 17 + n * 4) / (gae_ms * 1e-3) / 1e9},
