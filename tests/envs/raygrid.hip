@@ -1,0 +1,7 @@
+// Instantiates and registers the test-only ray-casting envs (see raygrid.h) in
+// the test env library.
+#include "mg/device/env_kernels.h"
+#include "raygrid.h"
+
+MG_DEFINE_ENV(RayGrid)
+MG_DEFINE_ENV(RayGridSplit)
