@@ -46,11 +46,11 @@ def kernel_avg_ms(times, k):
     return tot / cnt if cnt else float("nan")
 
 
-def bench_collect(kernel, n, T, steps, warmup, O, A, precision="fp32"):
+def bench_collect(kernel, n, T, steps, warmup, O, A, precision="fp32", layers=L):
     import metalgym_amd as mg
 
     gym = mg.Gym(kernel, n, 0)
-    model = mg.PPOModel(gym, horizon=T, precision=precision)
+    model = mg.PPOModel(gym, horizon=T, precision=precision, layers=layers)
     for _ in range(warmup):
         model.collect()
     sync()
@@ -92,11 +92,11 @@ def bench_random(n, T, reps, kernel="rollout_cartpole", hbm=True):
     return out
 
 
-def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32"):
+def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32", layers=L):
     import metalgym_amd as mg
 
     gym = mg.Gym(kernel, n, 0)
-    model = mg.PPOModel(gym, horizon=T, precision=precision)
+    model = mg.PPOModel(gym, horizon=T, precision=precision, layers=layers)
     model.collect()
     model.train(1)
     sync()
@@ -129,8 +129,9 @@ def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32"):
     dw = kernel_avg_ms(times, "train_dw") * 1e-3
     ad = kernel_avg_ms(times, "adam") * 1e-3
     count = model.pv.count
-    kern["train_rows_TFLOPs"] = round(B * (fwd_flop(O, A) + bwd_flop(O, A) - fwd_flop(O, A)) / tr / 1e12, 2)
-    kern["train_dw_TFLOPs"] = round(B * fwd_flop(O, A) / dw / 1e12, 2)
+    fw, bw = fwd_flop(O, A, layers), bwd_flop(O, A, layers)
+    kern["train_rows_TFLOPs"] = round(B * (fw + bw - fw) / tr / 1e12, 2)
+    kern["train_dw_TFLOPs"] = round(B * fw / dw / 1e12, 2)
     kern["adam_GBps"] = round(count * 28 / ad / 1e9, 1)
     out["kernels"] = kern
     return out
@@ -343,6 +344,13 @@ def main():
         extra["full_ppo_4096"] = bench_full("rollout_cartpole", 4096, 32, 5, O, A)
         extra["full_ppo_4096"]["vs_published_m4_296K"] = extra["full_ppo_4096"]["env_steps_per_s"] / 296e3
         extra["full_ppo_262144"] = bench_full("rollout_cartpole", 262144, 32, 1, O, A)
+        # the README's 1-block rows (published Apple M4 figures: 6.7 M collect, 496 K full loop)
+        _, _, dt1, _ = bench_collect("rollout_cartpole", 4096, 32, 20, 2, O, A, layers=1)
+        extra["collect_4096_1block"] = {"env_steps_per_s": 20 * 4096 * 32 / dt1,
+                                        "vs_published_m4_6.7M": 20 * 4096 * 32 / dt1 / 6.7e6}
+        extra["full_ppo_4096_1block"] = bench_full("rollout_cartpole", 4096, 32, 5, O, A, layers=1)
+        extra["full_ppo_4096_1block"]["vs_published_m4_496K"] = \
+            extra["full_ppo_4096_1block"]["env_steps_per_s"] / 496e3
         _, _, dtc, _ = bench_collect("rollout_cartpole_continuous", 262144, 32, 3, 1, 4, 1)
         extra["continuous_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtc}
         extra["continuous_full_ppo_65536"] = bench_full("rollout_cartpole_continuous", 65536, 32, 2, 4, 1)
