@@ -93,6 +93,11 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     using CS = CollectShape<M, Env::OBS_DIM, WIDE>;
     using LS = LdsState<Env, M, BF16, WIDE>;
     constexpr int O = Env::OBS_DIM, A = Env::ACT_DIM, HD = A + 1;
+    // the embed's observation width at compile time (its unrolled k loop reads
+    // a row's floats together: VoxelNav at 262144 envs 70.8 -> 66.0 ms) at
+    // 64-row and WIDE tiles; the others' register budgets it would overflow
+    // (VoxelNav's 32-row tiles with states in LDS: 44 VGPRs spilled)
+    constexpr int OE = M == 64 || WIDE ? O : 0;
     // parts of a split observation per env, spread over the whole workgroup
     // when the states sit in LDS or (WIDE) in device memory (0: the env lanes
     // call step())
@@ -175,12 +180,12 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
 
     for (uint32_t t = 0; t <= T; ++t) {
         if constexpr (BF16)
-            policy_forward_b<M, CS::W, HD>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward_b<M, CS::W, HD, OE>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
         else
             // global weight loads when the env states sit in LDS: there the
             // buffer loads' scalar descriptors cost the heightmap env more
             // spilling than they save (VoxelNav at 262144 envs, 135 -> 151 ms)
-            policy_forward<M, CS::W, !LS::USE, HD>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward<M, CS::W, !LS::USE, HD, OE>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
         if (envLane) {
             const float* h = sm.head + tid * HD;
             if (t == T) {  // bootstrap head for GAE and headValue()

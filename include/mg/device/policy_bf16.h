@@ -252,8 +252,8 @@ __device__ __forceinline__ void fwd_block_b(const mg_policy_view& pv, int l, Fwd
 }
 
 // Whole forward with bf16 GEMM operands: obs staged in obsL ([M][O], LDS) ->
-// head in headL ([M][HD], LDS). HDC: HD when known at compile time.
-template <int M, int W = 4, int HDC = 0>
+// head in headL ([M][HD], LDS). HDC, OC: HD and O when known at compile time.
+template <int M, int W = 4, int HDC = 0, int OC = 0>
 __device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, const SmallParams& sp, FwdSmemB<M>& sm,
                                                  FwdRegs<M, W>& R, const float* obsL, int O, float* headL, int HD) {
     using Stream = typename std::conditional<M == 16, TStreamB<M, W>, WStreamB<M, W>>::type;
@@ -261,8 +261,11 @@ __device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, const
     const int NC = (int)pv.hidden / kChunk;
     const Seq seq{&pv, NC};
     Stream ws;
+    // the embed first: its parameter reads (from global memory where the
+    // small parameters are not staged in LDS) then do not wait behind the
+    // weight stream's first loads (VoxelNav at 262144 envs: 66.0 -> 63.0 ms)
+    fwd_embed<M, W, OC>(sp.win, sp.bin, obsL, O, R);
     ws.start(2 * (int)pv.layers * NC, seq);
-    fwd_embed<M, W>(sp.win, sp.bin, obsL, O, R);
     for (uint32_t l = 0; l < pv.layers; ++l) {
         const float* g = sp.ln + 2 * kEmbed * l;
         fwd_layernorm<M, W>(sm, R, g, g + kEmbed, nullptr, nullptr, nullptr, sm.xb);
