@@ -11,7 +11,10 @@
 // when the tile's envs fit beside the forward's LDS (copied in and out by the
 // whole workgroup), else it is updated in place in device memory. Per env and
 // step the RNG order is: sample draw(s), reset draws if done, then step
-// (model/ppo.h:728-730, rollout.h:46-47).
+// (model/ppo.h:728-730, rollout.h:46-47). An env that declares a split
+// observation (OBS_SPLIT, env.h) has its states stepped by the env lanes,
+// which also write the observation's other floats; after a barrier all threads
+// of the workgroup compute the tile's OBS_SPLIT parts per env.
 #pragma once
 #include "policy_bf16.h"
 #include "sample.h"
