@@ -17,6 +17,7 @@
 // of the workgroup compute the tile's OBS_SPLIT parts per env.
 #pragma once
 #include "policy_bf16.h"
+#include "policy_split.h"
 #include "sample.h"
 
 namespace mg {
@@ -38,9 +39,19 @@ struct CollectShape {
     static constexpr int MIN_WG = M == 16 || (O > 32 && !WIDE) ? 1 : 2;  // workgroups per CU
 };
 
+// The forward of a tile: fp32 16-row tiles on 8 waves run the split layout
+// (split_forward16: no barrier per chunk, and the relu'd hidden chunk never
+// goes through LDS); the others stage each hidden chunk in LDS (policy.h,
+// policy_bf16.h).
+template <int M, int O, bool BF16>
+struct CollectFwd {
+    static constexpr bool SPLIT = !BF16 && M == 16 && CollectShape<M, O>::W == 8;
+    using Smem = std::conditional_t<SPLIT, SplitFwdSmem<8>, std::conditional_t<BF16, FwdSmemB<M>, FwdSmem<M>>>;
+};
+
 template <int M, int O, int HD, bool BF16>
 struct CollectSmem {
-    typename std::conditional<BF16, FwdSmemB<M>, FwdSmem<M>>::type fwd;
+    typename CollectFwd<M, O, BF16>::Smem fwd;
     float obs[M * O];
     float head[M * HD];
 };
@@ -110,6 +121,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     using SS = SmallStage<Env, M, BF16>;
     extern __shared__ float small_lds[];  // SS::floats(layers) floats when stage_small
     FwdRegs<M, CS::W> R;
+    std::conditional_t<CollectFwd<M, O, BF16>::SPLIT, SkStream<8 / CS::W>, char> wst;  // split forward's weights
 
     const int tid = threadIdx.x;
     const uint32_t n = a.n, T = a.horizon;
@@ -182,7 +194,9 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     __syncthreads();
 
     for (uint32_t t = 0; t <= T; ++t) {
-        if constexpr (BF16)
+        if constexpr (CollectFwd<M, O, BF16>::SPLIT)
+            split_forward16<CS::W, O>(a.policy, sp, sm.fwd, wst, t == 0, sm.obs, sm.head, HD);
+        else if constexpr (BF16)
             policy_forward_b<M, CS::W, HD, OE>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
         else
             // global weight loads when the env states sit in LDS: there the

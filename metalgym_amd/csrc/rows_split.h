@@ -1,30 +1,16 @@
 // The fp32 row pass of a PPO minibatch (the work of train_rows_kernel<false>:
-// forward recompute with capture, loss, backward dX chain, tile partials) with
-// the hidden units split over the waves, so that no chunk GEMM waits on a
-// barrier. Included by train_kernels.hip.
-//
-// A workgroup owns 16 rows on W waves (W = 4: one per SIMD; W = 8: two). Wave
-// w owns the S = 8 / W 16-unit strips 128 c + 16 (S w + s), s < S, of every
-// 128-wide chunk c and runs its chunks without synchronising with the other
-// waves:
-//   - the first GEMM computes its share of the chunk transposed, V^T = W0 X^T
-//     (16 units x 16 rows per strip on v_mfma_f32_16x16x4_f32, one
-//     accumulator chain per strip): the weights are the A operand, streamed
-//     from the fragment-tiled copies, and the block input X (the LN output, or
-//     dh in the backward) is the B operand, loaded from LDS into registers
-//     once per block;
-//   - the result registers, after relu (or the relu mask), are exactly the A
-//     operand of the second GEMM, which adds V W1 for this wave's units to a
-//     private 16 x 128 partial of the block output.
-// Once per block the W partials are added in LDS in wave order. Outside the
-// GEMMs each thread holds CPT = 32 / W consecutive columns of one row, so
-// LayerNorm, the head and the loss reduce over TPR = 4 W lanes (DPP and
-// readlane) and need no LDS round trip. The captures for the weight gradients
-// have the row-major layouts of train_rows_kernel<false>.
+// forward recompute with capture, loss, backward dX chain, tile partials) in
+// the hidden-unit split layout of include/mg/device/policy_split.h, so that no
+// chunk GEMM waits on a barrier. Included by train_kernels.hip. The loss
+// reduces over the same TPR lanes as LayerNorm. The captures for the weight
+// gradients have the row-major layouts of train_rows_kernel<false>.
 #pragma once
+#include "mg/device/policy_split.h"
 
 namespace mg {
 namespace dev {
+
+static_assert(kTR == kSplitRows, "a row-pass tile is a split tile");
 
 template <int W>
 struct SkShape {
@@ -59,209 +45,12 @@ struct alignas(16) SkSmem {
     static_assert((Sh::OBS + 1) * kEmbed <= W * kTR * kLds, "W_in and b_in fit the partial buffer");
 };
 
-// The chunk a wave's GEMM pair works on: the forward's blocks 0 .. L-1, then
-// the backward's L-1 .. 0, chunks in this wave's order. Wave w of workgroup b
-// starts block by block at chunk (w + b / 8) mod NC (workgroups go to the 8
-// XCDs round robin), so at any time the waves of a CU and the CUs of an XCD
-// stream different chunks' weights instead of all requesting the same lines
-// from L2 at once after a barrier. The order changes only the summation order
-// of a wave's partial over the chunks.
-struct SkPos {
-    int bwd, l, k;  // k: position in the wave's chunk order
-};
-
-// Where a chunk's operands live, from the contiguous block matrices (up_l at
-// float_group + 2 l E H, down_l right after it). Role 0 is W0 = up^T
-// (forward) or down as stored (backward), both [hidden][128]: the wave's S
-// strips 8 c + S w + s, each of eight 16-wide k-groups, all contiguous
-// (frag_index<16>, K = 128). Role 1 is W1 = down^T (forward) or up as stored
-// (backward), both [128][hidden]: k-groups 8 c + S w + s in each of the eight
-// 16-row strips (K = hidden), contiguous within a strip, the strips 16 hidden
-// rows apart.
-template <int S>
-struct SkSeq {
-    const float* fwd;  // frag_fwd16 + float_group
-    const float* bwd;  // frag_bwd16 + float_group
-    int L, nc, wave, rot;
-    uint32_t EH;  // 128 hidden: elements of one block matrix
-    __device__ __forceinline__ int chunk(const SkPos& p) const {
-        const int c = p.k + rot;
-        return c < nc ? c : c - nc;
-    }
-    __device__ __forceinline__ const float* role0(const SkPos& p) const {
-        const float* m = p.bwd ? bwd + (size_t)(2 * p.l + 1) * EH : fwd + (size_t)(2 * p.l) * EH;
-        return m + (size_t)(8 * chunk(p) + S * wave) * (16 * kEmbed);
-    }
-    __device__ __forceinline__ const float* role1(const SkPos& p) const {
-        const float* m = p.bwd ? bwd + (size_t)(2 * p.l) * EH : fwd + (size_t)(2 * p.l + 1) * EH;
-        return m + (size_t)chunk(p) * (16 * kChunk) + 256 * S * wave;
-    }
-    __device__ __forceinline__ uint32_t stride1() const { return EH / 8; }  // 16 hidden rows: 16 H
-    // The next chunk of the sequence; past its end, p itself.
-    __device__ __forceinline__ SkPos next(SkPos p) const {
-        if (++p.k < nc) return p;
-        p.k = 0;
-        if (!p.bwd) {
-            if (++p.l < L) return p;
-            p.bwd = 1;
-            p.l = L - 1;
-            return p;
-        }
-        if (--p.l >= 0) return p;
-        return SkPos{1, 0, nc - 1};
-    }
-};
-
-// The operand registers of both roles (8 S float4s each per lane): w0[8 s + g]
-// is k-group g of strip s, w1[S ct + s] strip s's k-group in column strip ct.
-// The loads are buffer loads with the k-group offset in an SGPR: the 64-bit
-// address arithmetic of global loads ran on the VALU between the MFMAs and
-// cost 3 us of the fp32 row pass. Each float4 is refilled for the same role
-// of the next chunk right after its MFMAs; past the end of the sequence a GEMM
-// reloads its own operand, so every path issues the same loads and the
-// vector-memory wait counts stay exact.
-template <int S>
-struct SkStream {
-    f32x4 w0[8 * S], w1[8 * S];
-
-    // one k-group: 16 bytes per lane of the 1 KB run at float offset off
-    __device__ __forceinline__ static f32x4 load(const float* p, uint32_t off) {
-        return buffer_load16(p, 16 * (threadIdx.x & 63), 4 * off);
-    }
-    __device__ __forceinline__ void start(const SkSeq<S>& seq, const SkPos& p) {
-        const float* a = seq.role0(p);
-        const float* b = seq.role1(p);
-        const uint32_t s1 = seq.stride1();
-#pragma unroll
-        for (int k = 0; k < 8 * S; ++k) w0[k] = load(a, 256 * k);
-#pragma unroll
-        for (int ct = 0; ct < 8; ++ct)
-#pragma unroll
-            for (int s = 0; s < S; ++s) w1[S * ct + s] = load(b, s1 * ct + 256 * s);
-    }
-    // acc[s] += W0 strip s . xb: acc[s] lane l register r = unit 4 (l / 16) +
-    // r of strip s, row l % 16; refills from nx (role 0 of the next chunk)
-    __device__ __forceinline__ void gemm0(f32x4 (&acc)[S], const f32x4 (&xb)[8], const float* nx) {
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int s = 0; s < S; ++s) acc[s] = mfma16x16x4(w0[8 * s + g][j], xb[g][j], acc[s]);
-#pragma unroll
-            for (int s = 0; s < S; ++s) w0[8 * s + g] = load(nx, 256 * (8 * s + g));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    // hp[ct] += v W1: v[s] is role 0's result for strip s; hp[ct] lane l
-    // register r = row 4 (l / 16) + r, column 16 ct + l % 16; refills from nx
-    // (role 1 of the next chunk, column strips s1 apart)
-    __device__ __forceinline__ void gemm1(f32x4 (&hp)[8], const f32x4 (&v)[S], const float* nx, uint32_t s1) {
-#pragma unroll
-        for (int ct = 0; ct < 8; ++ct) {
-#pragma unroll
-            for (int s = 0; s < S; ++s)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) hp[ct] = mfma16x16x4(v[s][j], w1[S * ct + s][j], hp[ct]);
-#pragma unroll
-            for (int s = 0; s < S; ++s) w1[S * ct + s] = load(nx, s1 * ct + 256 * s);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-};
-
-// The block input's B-operand registers: lane (n = l % 16, q = l / 16) holds
-// X[n][16 g + 4 q .. + 3] for k-group g (the K order of the fragment layout).
-__device__ __forceinline__ void sk_load_input(const float* xs, f32x4 (&xb)[8]) {
-    const int lane = threadIdx.x & 63;
-    const float* p = xs + (lane & 15) * kLds + 4 * (lane >> 4);
-#pragma unroll
-    for (int g = 0; g < 8; ++g) xb[g] = *reinterpret_cast<const f32x4*>(p + 16 * g);
-}
-
-// A thread's CPT consecutive columns of one row.
-template <int NV>
-struct RowVec {
-    float c[4 * NV];
-    __device__ __forceinline__ float& operator[](int i) { return c[i]; }
-    __device__ __forceinline__ float operator[](int i) const { return c[i]; }
-};
-
-template <int NV>
-__device__ __forceinline__ RowVec<NV> rv_load(const float* p) {
-    RowVec<NV> r;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const f32x4 t = *reinterpret_cast<const f32x4*>(p + 4 * i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) r.c[4 * i + j] = t[j];
-    }
-    return r;
-}
-template <int NV>
-__device__ __forceinline__ void rv_store(float* p, const RowVec<NV>& r) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-        *reinterpret_cast<f32x4*>(p + 4 * i) = f32x4{r.c[4 * i], r.c[4 * i + 1], r.c[4 * i + 2], r.c[4 * i + 3]};
-}
-template <int NV>
-__device__ __forceinline__ RowVec<NV> rv_zero() {
-    RowVec<NV> r;
-#pragma unroll
-    for (int i = 0; i < 4 * NV; ++i) r.c[i] = 0.0f;
-    return r;
-}
-template <int NV>
-__device__ __forceinline__ RowVec<NV> rv_add(const RowVec<NV>& a, const RowVec<NV>& b) {
-    RowVec<NV> r;
-#pragma unroll
-    for (int i = 0; i < 4 * NV; ++i) r.c[i] = a.c[i] + b.c[i];
-    return r;
-}
-
 // The block output: this wave's partial to LDS, a barrier, then the thread's
 // row and columns summed over the waves in order.
 template <int W>
 __device__ __forceinline__ RowVec<SkShape<W>::NV> sk_reduce(SkSmem<W>& L, const f32x4 (&hp)[8], int wave, int row,
                                                             int c0) {
-    constexpr int NV = SkShape<W>::NV;
-    const int lane = threadIdx.x & 63;
-    float* rw = L.red[wave] + 4 * (lane >> 4) * kLds + (lane & 15);
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) rw[r * kLds + 16 * ct] = hp[ct][r];
-    __syncthreads();
-    RowVec<NV> s = rv_load<NV>(L.red[0] + row * kLds + c0);
-#pragma unroll
-    for (int w = 1; w < W; ++w) s = rv_add(s, rv_load<NV>(L.red[w] + row * kLds + c0));
-    return s;
-}
-
-// model/layernorm.metal:10-71 on a row held by TPR lanes (CPT columns each).
-template <int TPR, int NV>
-__device__ __forceinline__ void sk_layernorm(const RowVec<NV>& h, const float* gamma, const float* beta, int c0,
-                                             RowVec<NV>& x, RowVec<NV>& xn, float& sd) {
-    constexpr int CPT = 4 * NV;
-    float s = h[0];
-#pragma unroll
-    for (int c = 1; c < CPT; ++c) s += h[c];
-    s = group_sum<TPR>(s);
-    const float mean = s / (float)kEmbed;
-    float q = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-        const float d = h[c] - mean;
-        q += d * d;
-    }
-    q = group_sum<TPR>(q);
-    sd = sqrtf(q / (float)kEmbed + 1e-5f);
-    const float rstd = 1.0f / sd;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-        xn[c] = (h[c] - mean) * rstd;
-        x[c] = gamma[c0 + c] * xn[c] + beta[c0 + c];
-    }
+    return sk_reduce_buf<W, SkShape<W>::NV>(&L.red[0][0], hp, wave, row, c0);
 }
 
 // model/layernorm.metal:74-127 on a row: g is the gradient at the LN output,
