@@ -228,7 +228,8 @@ def pmc_traffic():
 
 def profile_pass(which):
     """Short runs of each kernel for rocprofv3 (--kernel-trace / --pmc): the
-    262144-env collect and random rollout, 64 train minibatches, and one 1 GiB
+    262144-env collect and random rollout, 64 train minibatches, the 4096-env
+    collect ("all"; its 16-row tiles), and one 1 GiB
     device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters
     ("all" adds 64 copies of the Adam step's byte count, its size floor).
     "bf16": the collect and the minibatches in bf16 mode, and the copy.
@@ -258,6 +259,14 @@ def profile_pass(which):
             sync()
             print(f"profile: 64 {precision} train minibatches of 4096 rows", flush=True)
         del model, gym
+        if which == "all":  # 16-row tiles (the split forward)
+            gym = mg.Gym("rollout_cartpole", 4096, 0)
+            model = mg.PPOModel(gym, horizon=T)
+            for _ in range(3):
+                model.collect()
+            sync()
+            print("profile: 3 fp32 collects of 4096 x 32", flush=True)
+            del model, gym
     if which in ("random", "all"):
         gym = mg.Gym("rollout_cartpole", n, 0)
         bufs = gym.rollout_random(T)
