@@ -19,8 +19,10 @@
 // (rngNext & 4095) for the agent cell and then the goal cell, at most 64 each;
 // if all 64 land on occupied cells the last drawn cell is cleared.
 //
-// The state is 4 KB per env, so the rollout kernels update it in place in
-// device memory instead of holding it in registers.
+// The state is 4 KB per env, so the kernels keep it in device memory (or a
+// rollout's LDS) instead of registers. The 27 neighbourhood cells are declared
+// a split observation (OBS_SPLIT, env.h): independent gathers from the grid,
+// which the kernels spread over a workgroup's threads.
 #pragma once
 #include "../env.h"
 
@@ -89,18 +91,26 @@ struct VoxelNav16 {
         s.steps = 0;
     }
 
-    MG_HD static void observe(const State& s, Obs& obs) {
-        int k = 0;
-        for (int dz = -1; dz <= 1; ++dz)
-            for (int dy = -1; dy <= 1; ++dy)
-                for (int dx = -1; dx <= 1; ++dx)
-                    obs.cells[k++] = occupied(s, s.px + dx, s.py + dy, s.pz + dz) ? 1.0f : 0.0f;
+    static constexpr uint32_t OBS_SPLIT = 27;
+
+    // neighbourhood cell k = 9 (dz + 1) + 3 (dy + 1) + (dx + 1)
+    MG_HD static float observePart(const State& s, uint32_t k) {
+        const int dx = (int)(k % 3u) - 1, dy = (int)(k / 3u % 3u) - 1, dz = (int)(k / 9u) - 1;
+        return occupied(s, s.px + dx, s.py + dy, s.pz + dz) ? 1.0f : 0.0f;
+    }
+
+    MG_HD static void observeRest(const State& s, Obs& obs) {
         obs.goal[0] = (float)(s.gx - s.px) / 15.0f;
         obs.goal[1] = (float)(s.gy - s.py) / 15.0f;
         obs.goal[2] = (float)(s.gz - s.pz) / 15.0f;
     }
 
-    MG_HD static void step(State& s, Action action, Obs& obs, float& reward, uint8_t& done) {
+    MG_HD static void observe(const State& s, Obs& obs) {
+        for (uint32_t k = 0; k < OBS_SPLIT; ++k) obs.cells[k] = observePart(s, k);
+        observeRest(s, obs);
+    }
+
+    MG_HD static void stepState(State& s, Action action, float& reward, uint8_t& done) {
         int a = action < 0 ? 0 : (action > 5 ? 5 : action);
         int sign = (a & 1) ? -1 : 1;
         int axis = a >> 1;
@@ -117,6 +127,10 @@ struct VoxelNav16 {
         bool atGoal = s.px == s.gx && s.py == s.gy && s.pz == s.gz;
         reward = atGoal ? 1.0f : (blocked ? -0.1f : -0.01f);
         done = (atGoal || s.steps >= MAX_STEPS) ? 1 : 0;
+    }
+
+    MG_HD static void step(State& s, Action action, Obs& obs, float& reward, uint8_t& done) {
+        stepState(s, action, reward, done);
         observe(s, obs);
     }
 };
