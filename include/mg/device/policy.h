@@ -315,17 +315,51 @@ __device__ __forceinline__ void store_tile_g(const AccTile<M, W>& acc, float* gl
     });
 }
 
-// model/input.metal:11-27: h = b_in + sum_k obs[k] W_in[k], in k order.
+// model/input.metal:11-27: h = b_in + sum_k obs[k] W_in[k].
 // obsL is [M][O] in LDS; Win ([O][128]) and bias ([128]) are in global memory
-// or LDS. OC: O when known at compile time; then the k loop is unrolled and a
-// row's consecutive observation floats are read together (VoxelNav16's 30
-// floats: the embed phase of a 64-row collect step took 64.6 K cycles read one
-// float at a time).
+// or LDS. OC: O when known at compile time.
+// 32- and 64-row tiles: the product on v_mfma_f32_32x32x2_f32 straight into
+// the residual accumulators (A = obs rows, B = W_in columns, k = 2 s + lane /
+// 32, zero past O). Per element and k a lane otherwise reads the row's
+// observation float from LDS: 960 reads per lane for VoxelNav16's 30 floats,
+// whose embed phase then took 111 K cycles of a 64-row collect step (and its
+// LN0 130 K, waiting at the barrier for the slowest wave) against CartPole's
+// 2.5 K and 34 K. 16-row tiles (8 elements or fewer per lane): in k order,
+// the k loop unrolled when OC is known (a row's consecutive floats read
+// together).
 template <int M, int W = 4, int OC = 0>
 __device__ __forceinline__ void fwd_embed(const float* Win, const float* bias, const float* obsL, int O,
                                           FwdRegs<M, W>& R) {
     for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) { R.h[rt][ct][r] = bias[col]; });
-    if constexpr (OC > 0) {
+    using S = Shape<M, W>;
+    if constexpr (S::MT == 32) {
+        const int lane = threadIdx.x & 63, n = lane & 31, q = lane >> 5;
+        const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const int On = OC > 0 ? OC : O;
+        const int steps = (On + 1) / 2;
+        constexpr int kUnroll = OC > 0 ? (OC + 1) / 2 : 1;
+#pragma unroll kUnroll
+        for (int st = 0; st < steps; ++st) {
+            const int k = 2 * st + q;
+            const bool in = k < On;
+            const int kk = in ? k : 0;  // every read in bounds; the padding step's operands are zeroed
+            float a[S::RT], b[S::CT];
+#pragma unroll
+            for (int rt = 0; rt < S::RT; ++rt) {
+                const float v = obsL[(S::MT * rt + n) * On + kk];
+                a[rt] = in ? v : 0.0f;
+            }
+#pragma unroll
+            for (int ct = 0; ct < S::CT; ++ct) {
+                const float v = Win[kk * kEmbed + S::SW * wave + S::MT * ct + n];
+                b[ct] = in ? v : 0.0f;
+            }
+#pragma unroll
+            for (int rt = 0; rt < S::RT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < S::CT; ++ct) R.h[rt][ct] = mfma32x32x2(a[rt], b[ct], R.h[rt][ct]);
+        }
+    } else if constexpr (OC > 0) {
 #pragma unroll
         for (int k = 0; k < OC; ++k) {
             for_each_elem<M, W>([&](int rt, int ct, int r, int row, int col) {
