@@ -129,28 +129,38 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     const float* lnp = pv.params + pv.off_ln_gamma[0];
     const int n_obs = M * O, n_wh = kEmbed * HD, n_win = O * kEmbed, n_ln = (NL + 1) * 2 * kEmbed;
     {
+        // W_in as float4s, all of a thread's issued with the other first loads
+        // (VoxelNav16's 3840 floats four loads at a time took two memory round
+        // trips of the start-up)
+        constexpr int NW4 = (Sh::OBS * kEmbed / 4 + NT - 1) / NT;
+        const int n_win4 = n_win / 4;  // O x 128 floats
         const float o0 = tid < n_obs ? a.obs_slots[g0 * O + tid] : 0.0f;
         const float h0 = tid < n_wh ? pv.params[pv.off_head + tid] : 0.0f;
-        const float w0 = tid < n_win ? pv.params[pv.off_in_w + tid] : 0.0f;
+        f32x4 wv[NW4];
+#pragma unroll
+        for (int u = 0; u < NW4; ++u) {
+            const int i4 = tid + u * NT;
+            wv[u] = i4 < n_win4 ? *reinterpret_cast<const f32x4*>(pv.params + pv.off_in_w + 4 * i4)
+                                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
         const float b0 = tid < kEmbed ? pv.params[pv.off_in_b + tid] : 0.0f;
         const float l0 = tid < n_ln ? lnp[tid] : 0.0f;
         const float l1 = tid + NT < n_ln ? lnp[tid + NT] : 0.0f;
         if (tid < n_obs) L.obs[tid] = o0;
         if (tid < n_wh) L.wh[tid] = h0;
-        if (tid < n_win) winL[tid] = w0;
+#pragma unroll
+        for (int u = 0; u < NW4; ++u)
+            if (tid + u * NT < n_win4) *reinterpret_cast<f32x4*>(winL + 4 * (tid + u * NT)) = wv[u];
         if (tid < kEmbed) binL[tid] = b0;
         if (tid < n_ln) L.ln[tid] = l0;
         if (tid + NT < n_ln) L.ln[tid + NT] = l1;
     }
-    // the rest, four elements' loads ahead of their stores (VoxelNav16's
-    // 3840-float W_in: 51.0 -> 50.4 us per minibatch; CartPole's arrays need
-    // no second element)
+    // the rest, four elements' loads ahead of their stores (CartPole's arrays
+    // need no second element)
 #pragma unroll 4
     for (int idx = tid + NT; idx < n_obs; idx += NT) L.obs[idx] = a.obs_slots[g0 * O + idx];
 #pragma unroll 4
     for (int idx = tid + NT; idx < n_wh; idx += NT) L.wh[idx] = pv.params[pv.off_head + idx];
-#pragma unroll 4
-    for (int idx = tid + NT; idx < n_win; idx += NT) winL[idx] = pv.params[pv.off_in_w + idx];
 #pragma unroll 4
     for (int idx = tid + 2 * NT; idx < n_ln; idx += NT) L.ln[idx] = lnp[idx];
     float an, oldLp, ret;
