@@ -39,15 +39,18 @@ def test_random_rollout_bit_exact(mg, orc, env, n, steps, seed):
     assert dn.any(), "no episode ended: the test does not exercise resets"
 
 
-@pytest.mark.parametrize("n,steps,reps,seed", [
-    (4100, 40, 7, 4),     # 8 envs per workgroup, the last workgroup partial
-    (33000, 20, 13, 5),   # 16 envs per workgroup, the last workgroup partial
+@pytest.mark.parametrize("env,n,steps,reps,seed", [
+    ("voxelnav", 4100, 40, 7, 4),      # 8 envs per workgroup, the last workgroup partial
+    ("voxelnav", 33000, 20, 13, 5),    # 16 envs per workgroup, the last workgroup partial
+    ("voxelnav16", 4100, 40, 7, 6),    # 4 KB states, 8 per workgroup (33 KB of LDS)
+    ("voxelnav16", 33000, 20, 13, 7),  # 16 per workgroup (66 KB of LDS)
 ])
-def test_split_rollout_sizes_bit_exact(mg, orc, n, steps, reps, seed):
-    """VoxelNav's split-observation rollout (its ray casts spread over each
-    workgroup) at the env counts that give 8 and 16 envs per workgroup, run past
-    the 250-step cap so that every env resets at least once."""
-    eid, kernel = ENVS["voxelnav"]
+def test_split_rollout_sizes_bit_exact(mg, orc, env, n, steps, reps, seed):
+    """The split-observation rollouts (VoxelNav's ray casts, VoxelNav16's
+    neighbourhood cells, spread over each workgroup) at the env counts that
+    give 8 and 16 envs per workgroup, run past the 250- and 256-step caps so
+    that every env resets at least once."""
+    eid, kernel = ENVS[env]
     gym = mg.Gym(kernel, n, seed)
     g = orc.GymState(eid, n, seed)
     bufs = None
