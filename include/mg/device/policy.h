@@ -389,17 +389,25 @@ __device__ __forceinline__ float row_sum(float (&t)[N]) {
     }
 }
 
+template <int M, int W, int HDC>
+__device__ __forceinline__ void fwd_head_regs(const float (&x)[kEmbed / (Shape<M, W>::NT / M)], const float* Wh,
+                                              float* headL, int HD);
+
 // model/layernorm.metal:10-71 on the register tile; the result goes to sm.xs.
 // If xn_out/sd_out/x_out are given, the normalised values, the standard
 // deviation and the output are also written there ([M][128], [M], [M][128],
 // row-major; global memory or LDS) for the backward pass; if xb_out is given,
 // the output rounded to bfloat16 goes there too ([M] rows of stride kLdsB).
-// Smem is any shared-memory layout with an fp32 xs tile.
+// Smem is any shared-memory layout with an fp32 xs tile. HF >= 0: the final
+// LN, followed by the head straight from the registers (fwd_head_regs with
+// HDC = HF, head weights Wh, output headL, HD columns) instead of through xs
+// and a barrier; xs then keeps the LN input.
 constexpr int kLdsB = kEmbed + 8;  // LDS row stride of a bfloat16 tile (elements)
-template <int M, int W = 4, class Smem>
+template <int M, int W = 4, class Smem, int HF = -1>
 __device__ __forceinline__ void fwd_layernorm(Smem& sm, const FwdRegs<M, W>& R, const float* gamma,
                                               const float* beta, float* xn_out = nullptr, float* sd_out = nullptr,
-                                              float* x_out = nullptr, uint16_t* xb_out = nullptr) {
+                                              float* x_out = nullptr, uint16_t* xb_out = nullptr,
+                                              const float* Wh = nullptr, float* headL = nullptr, int HD = 0) {
     constexpr int TPR = Shape<M, W>::NT / M;  // threads per row
     constexpr int CPT = kEmbed / TPR;         // columns per thread
     static_assert(CPT % 4 == 0, "float4 columns");
@@ -432,6 +440,7 @@ __device__ __forceinline__ void fwd_layernorm(Smem& sm, const FwdRegs<M, W>& R, 
     const float var = q / (float)kEmbed;
     const float sd = sqrtf(var + 1e-5f);
     const float rstd = 1.0f / sd;
+    float oall[CPT];  // the output, for a fused head
 #pragma unroll
     for (int c = 0; c < CPT; c += 4) {
         f32x4 o, xn;
@@ -439,8 +448,9 @@ __device__ __forceinline__ void fwd_layernorm(Smem& sm, const FwdRegs<M, W>& R, 
         for (int u = 0; u < 4; ++u) {
             xn[u] = (x[c + u] - mean) * rstd;
             o[u] = gamma[c0 + c + u] * xn[u] + beta[c0 + c + u];
+            oall[c + u] = o[u];
         }
-        *reinterpret_cast<f32x4*>(xr + c) = o;
+        if constexpr (HF < 0) *reinterpret_cast<f32x4*>(xr + c) = o;
         if (xn_out) *reinterpret_cast<f32x4*>(xn_out + row * kEmbed + c0 + c) = xn;
         if (xb_out) {
             uint16_t hb[4];
@@ -455,7 +465,11 @@ __device__ __forceinline__ void fwd_layernorm(Smem& sm, const FwdRegs<M, W>& R, 
         }
     }
     if (sd_out && part == 0) sd_out[row] = sd;
-    __syncthreads();
+    if constexpr (HF >= 0) {
+        fwd_head_regs<M, W, HF>(oall, Wh, headL, HD);  // ends with a barrier
+    } else {
+        __syncthreads();
+    }
 }
 
 // The forward's GEMM sequence: for block l and chunk c, GEMM 2 (l NC + c)
@@ -502,26 +516,21 @@ __device__ __forceinline__ void fwd_block(const mg_policy_view& pv, int l, FwdSm
     }
 }
 
-// model/linear.metal:17-37: head[row][j] = sum_k xs[row][k] W_head[k][j] for
+// model/linear.metal:17-37: head[row][j] = sum_k x[row][k] W_head[k][j] for
 // j < HD, into headL ([M][HD] in LDS). Wh is W_head ([128][HD], global memory
 // or LDS). Ends with a barrier.
 // HDC: the head width when known at compile time (0: runtime HD only). Then a
 // thread's block of W_head is read as float4s, G columns at a time (24 loads
 // instead of 96 at 64-row tiles of a 3-column head: the 262144-env collect
 // 34.70 -> 34.19 ms).
-template <int M, int W = 4, int HDC = 0, class Smem>
-__device__ __forceinline__ void fwd_head(const float* Wh, Smem& sm, float* headL, int HD) {
+// fwd_head_regs: x is this thread's CPT columns of its row (the LayerNorm's
+// thread layout, TPR threads per row).
+template <int M, int W, int HDC>
+__device__ __forceinline__ void fwd_head_regs(const float (&x)[kEmbed / (Shape<M, W>::NT / M)], const float* Wh,
+                                              float* headL, int HD) {
     constexpr int TPR = Shape<M, W>::NT / M, CPT = kEmbed / TPR;
     const int tid = threadIdx.x, row = tid / TPR, part = tid % TPR, c0 = part * CPT;
     const float* wp = Wh + c0 * HD;
-    const float* xr = sm.xs + row * kLds + c0;
-    float x[CPT];
-    static_assert(CPT % 4 == 0, "float4 columns");
-#pragma unroll
-    for (int c = 0; c < CPT; c += 4) {  // float4 reads: no bank conflicts between lanes
-        const f32x4 v = *reinterpret_cast<const f32x4*>(xr + c);
-        x[c] = v[0], x[c + 1] = v[1], x[c + 2] = v[2], x[c + 3] = v[3];
-    }
     // G columns at a time: the largest power of two whose G x HDC weights fit
     // 96 registers and start 16-byte aligned; heads of up to 4 columns only
     // (wider ones made VoxelNav16's collect spill)
@@ -563,6 +572,23 @@ __device__ __forceinline__ void fwd_head(const float* Wh, Smem& sm, float* headL
     __syncthreads();
 }
 
+
+// The head from the LN output in sm.xs (x = xs rows).
+template <int M, int W = 4, int HDC = 0, class Smem>
+__device__ __forceinline__ void fwd_head(const float* Wh, Smem& sm, float* headL, int HD) {
+    constexpr int TPR = Shape<M, W>::NT / M, CPT = kEmbed / TPR;
+    const int tid = threadIdx.x, row = tid / TPR, part = tid % TPR, c0 = part * CPT;
+    const float* xr = sm.xs + row * kLds + c0;
+    float x[CPT];
+    static_assert(CPT % 4 == 0, "float4 columns");
+#pragma unroll
+    for (int c = 0; c < CPT; c += 4) {  // float4 reads: no bank conflicts between lanes
+        const f32x4 v = *reinterpret_cast<const f32x4*>(xr + c);
+        x[c] = v[0], x[c + 1] = v[1], x[c + 2] = v[2], x[c + 3] = v[3];
+    }
+    fwd_head_regs<M, W, HDC>(x, Wh, headL, HD);
+}
+
 // Where a forward reads its small parameters: W_in [O][128], b_in, the LN
 // parameters (LN l: gamma at ln + 256 l, beta at ln + 256 l + 128; the arena
 // keeps them contiguous) and W_head [128][HD]; the arena itself, or copies in
@@ -601,8 +627,7 @@ __device__ __forceinline__ void policy_forward(const mg_policy_view& pv, const S
         fwd_block<M, W, false, 1, Seq>(pv, (int)l, sm, R, ws, nullptr, seq);
     }
     const float* g = sp.ln + 2 * kEmbed * pv.layers;
-    fwd_layernorm<M, W>(sm, R, g, g + kEmbed);
-    fwd_head<M, W, HDC>(sp.wh, sm, headL, HD);
+    fwd_layernorm<M, W, FwdSmem<M>, HDC>(sm, R, g, g + kEmbed, nullptr, nullptr, nullptr, nullptr, sp.wh, headL, HD);
 }
 
 }  // namespace dev

@@ -272,8 +272,7 @@ __device__ __forceinline__ void policy_forward_b(const mg_policy_view& pv, const
         fwd_block_b<M, W, false, 1, Seq>(pv, (int)l, sm, R, ws, nullptr, seq);
     }
     const float* g = sp.ln + 2 * kEmbed * pv.layers;
-    fwd_layernorm<M, W>(sm, R, g, g + kEmbed);
-    fwd_head<M, W, HDC>(sp.wh, sm, headL, HD);
+    fwd_layernorm<M, W, FwdSmemB<M>, HDC>(sm, R, g, g + kEmbed, nullptr, nullptr, nullptr, nullptr, sp.wh, headL, HD);
 }
 
 }  // namespace dev
