@@ -109,9 +109,16 @@ typedef struct mg_rollout_args {
  * MG_PRECISION_BF16, frag_fwd32_bf and frag_fwd16_bf hold up^T and down^T and
  * frag_bwd16_bf up and down, rounded to bfloat16 (16-bit patterns), in the
  * operand order of the bf16 instructions (32x32x16 and 16x16x32: k-groups of
- * 16 and 32, each lane 8 consecutive k); otherwise they are NULL. The library derives all of them
- * from params at creation, in every Adam step and in mg_ppo_set_params /
- * mg_ppo_params_updated; the fused kernels read the matrices from them. */
+ * 16 and 32, each lane 8 consecutive k); otherwise they are NULL. The fused kernels read the
+ * matrices from them. The library derives all of them from params at creation and in
+ * mg_ppo_set_params / mg_ppo_params_updated. A train step (mg_ppo_train, mg_ppo_train_block,
+ * mg_ppo_train_block_noalloc) rewrites only the copies its own kernels read next (frag_fwd16
+ * and frag_bwd16; in bf16 mode their bf16 versions) and leaves the others (frag_fwd32, and in
+ * bf16 mode the fp32 copies and frag_fwd32_bf) behind params until the next mg_ppo_policy,
+ * mg_ppo_collect or mg_ppo_forward re-derives them. The pointers never change, so a view stays
+ * valid for the model's life, but its copies are current only after one of those calls: a
+ * caller that launches kernels with a view after training (an env's mg_env_desc.collect, say)
+ * calls mg_ppo_policy first. */
 enum { MG_PRECISION_FP32 = 0, MG_PRECISION_BF16 = 1 };
 typedef struct mg_policy_view {
     float* params;
@@ -318,8 +325,10 @@ int mg_ppo_train_block(mg_ppo* model, uint32_t block);
  * the array when it is NULL. Asynchronous on the gym's stream; the Adam step
  * count and its bias corrections are taken at call time. Every call on one
  * device shares the array: calls that overlap on one device (two streams, two
- * threads) race. mg_ppo_last_stats, mg_ppo_train_stats and
- * mg_ppo_last_order are not updated. */
+ * threads) race. mg_ppo_last_stats, mg_ppo_train_stats, mg_ppo_last_order
+ * and mg_ppo_train_capture are not updated (the captures of a no-alloc call
+ * live in the array; mg_ppo_train_capture keeps returning those of the last
+ * mg_ppo_train or mg_ppo_train_block, or MG_ERR_STATE if there was none). */
 int mg_ppo_train_block_noalloc(mg_ppo* model, uint32_t block, float* stats_out);
 /* model/ppo.h:628-634: policy forward on `rows` obs rows (device pointer) into
  * the model's head buffer. Blocking. */
@@ -341,8 +350,9 @@ int mg_ppo_set_params(mg_ppo* model, const float* host, uint32_t count);
 /* Re-derives the fragment-tiled copies after the caller wrote params through
  * the device view. */
 int mg_ppo_params_updated(mg_ppo* model);
-/* Activation captures of the last train minibatch (the row pass writes them
- * for the weight gradients), for tests and debugging; no reference
+/* Activation captures of the last minibatch of mg_ppo_train or
+ * mg_ppo_train_block (the row pass writes them for the weight gradients;
+ * mg_ppo_train_block_noalloc leaves them unchanged), for tests and debugging; no reference
  * counterpart (the reference keeps its activations in internal buffers,
  * model/ppo.h:355-372). which = MG_CAPTURE_*: the LN outputs entering each
  * block ([layers][B][128]), the relu'd hidden activations ([layers][B][hidden]),

@@ -114,8 +114,9 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     constexpr int OE = M == 64 || WIDE ? O : 0;
     // parts of a split observation per env, spread over the whole workgroup
     // when the states sit in LDS or (WIDE) in device memory (0: the env lanes
-    // call step())
-    constexpr uint32_t KS = LS::USE || WIDE ? Tr::OBS_SPLIT : 0;
+    // call step()). A State held in registers is written back only at the end,
+    // so the other threads could not read it: such an env always calls step().
+    constexpr uint32_t KS = LS::USE || (WIDE && !Tr::STATE_IN_REGISTERS) ? Tr::OBS_SPLIT : 0;
     __shared__ CollectSmem<M, O, HD, BF16> sm;
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     using SS = SmallStage<Env, M, BF16>;

@@ -24,11 +24,11 @@
 //
 // promises that step(s, a, obs, r, d) is stepState(s, a, r, d) followed by
 // obs float k = observePart(s, k) for every k < K and observeRest(s, obs),
-// with the same results. The kernels then spread a tile's K parts per env over
-// all of its workgroup's threads: collect (states in LDS, or in device memory
-// at two workgroups per CU) and, for a State of more than 64 bytes whose size
-// is a multiple of 4, the rollouts (the tile's states staged in LDS). The
-// other shapes call step().
+// with the same results. For a State of more than 64 bytes (smaller ones live
+// in the env lane's registers) the kernels then spread a tile's K parts per env
+// over all of its workgroup's threads: collect (states in LDS, or in device
+// memory at two workgroups per CU) and, where the size is a multiple of 4, the
+// rollouts (the tile's states staged in LDS). The other shapes call step().
 //
 // This mirrors the reference's Env template (README.md:21-66; rollout.h:31-54):
 // same member names, same reset/step contract, one struct instead of a Metal

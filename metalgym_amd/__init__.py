@@ -8,7 +8,9 @@ if the library has not been built, importing ``lib()`` raises.
 """
 from ._capi import (  # noqa: F401
     LIB_PATH,
+    COLLECT_FN,
     CapiError,
+    CollectArgs,
     Gym,
     KernelTimes,
     LossStats,
@@ -18,7 +20,10 @@ from ._capi import (  # noqa: F401
     PolicyView,
     DeviceBuffer,
     build,
+    d2h,
+    env_desc,
     env_names,
+    h2d,
     lib,
     timing_enable,
     timing_get,

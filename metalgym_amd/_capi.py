@@ -45,6 +45,16 @@ class PolicyView(C.Structure):
     ]
 
 
+class CollectArgs(C.Structure):
+    """mg_collect_args: the launch arguments of an env's fused collect kernel."""
+    _fields_ = [("stream", P), ("policy", PolicyView), ("n", u32), ("horizon", u32), ("first", u32),
+                ("reserved", u32), ("state", P), ("rng", P), ("done", P), ("obs_slots", P), ("action_slots", P),
+                ("logp_slots", P), ("value_slots", P), ("reward_slots", P), ("done_slots", P), ("head_out", P)]
+
+
+COLLECT_FN = C.CFUNCTYPE(C.c_int, C.POINTER(CollectArgs))
+
+
 class GymBuffers(C.Structure):
     _fields_ = [("stream", P), ("env", C.POINTER(EnvDesc)), ("n", u32), ("seed", u32), ("state", P), ("actions", P),
                 ("obs", P), ("reward", P), ("done", P), ("rng", P)]
@@ -359,6 +369,12 @@ class PPOModel:
         s = PPOSlots()
         check(lib().mg_ppo_slots_get(self.h, C.byref(s)))
         self.slots = s
+
+    def policy(self) -> PolicyView:
+        """mg_ppo_policy: the device view, its fragment-tiled copies current."""
+        pv = PolicyView()
+        check(lib().mg_ppo_policy(self.h, C.byref(pv)))
+        return pv
 
     def destroy(self) -> None:
         if self.h:

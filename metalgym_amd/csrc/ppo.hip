@@ -134,7 +134,9 @@ int ensure_train_ws(mg_ppo* p, uint32_t minibatches) {
         train_ws_bytes(p->pv, p->B, &bytes);
         int rc = device_alloc(&p->ws_base, bytes, "PPOModel train workspace");
         if (rc) return rc;
-        // tile partials of padding elements are never written and must read as 0
+        // every element the kernels read is written first (the only padding,
+        // after log_std, gets explicit zeros), so this clear only makes a fresh
+        // workspace deterministic to inspect through mg_ppo_train_capture
         MG_HIP(hipMemsetAsync(p->ws_base, 0, bytes, p->gym->stream), "train workspace clear");
         train_ws_bind(p->pv, p->B, p->ws_base, &p->ws);
     }
@@ -260,6 +262,12 @@ int validate_config(const mg_env_desc* env, uint32_t n, const mg_ppo_config* c, 
     MG_CHECK(B % 64 == 0 && n % B == 0, MG_ERR_INVALID, "PPOModel: minibatch %u must be a multiple of 64 that divides %u",
              B, n);
     MG_CHECK((uint64_t)n * (c->horizon + 1) < (1ull << 31), MG_ERR_INVALID, "PPOModel: n * (horizon + 1) too large");
+    // the weight-gradient kernels address a capture of B rows with 32-bit
+    // byte offsets (buffer loads): B * max(hidden, 128) * 4 must stay below 2^31
+    const uint64_t widest = std::max<uint64_t>((uint64_t)c->embed * c->scale, MG_EMBED);
+    MG_CHECK((uint64_t)B * widest * 4 < (1ull << 31), MG_ERR_INVALID,
+             "PPOModel: minibatch %u x hidden %u is too large (the captures' byte offsets must fit 31 bits)", B,
+             c->embed * c->scale);
     if (B_out) *B_out = B;
     return MG_OK;
 }

@@ -77,6 +77,8 @@ def cfg(**kw):
 def test_valid_config_passes(mg):
     assert mg.lib().mg_ppo_check_config(b"rollout_cartpole", 4096, C.byref(cfg())) == 0
     assert mg.lib().mg_ppo_check_config(b"rollout_voxelnav16", 262144, C.byref(cfg())) == 0
+    # the largest minibatch whose captures keep 32-bit offsets at hidden 1024
+    assert mg.lib().mg_ppo_check_config(b"rollout_cartpole", 262144, C.byref(cfg(minibatch=262144, scale=8))) == 0
 
 
 # model/ppo.h:290-298: every constructor validation failure, forced from the host
@@ -89,6 +91,7 @@ def test_valid_config_passes(mg):
     (4096, dict(scale=0), b"scale"),
     (4096, dict(minibatch=100), b"minibatch"),
     (4096, dict(minibatch=8192), b"minibatch"),
+    (524288, dict(minibatch=524288, scale=8), b"31 bits"),  # captures of 2 GiB: beyond 32-bit offsets
 ])
 def test_config_validation(mg, n, kw, needle):
     rc = mg.lib().mg_ppo_check_config(b"rollout_cartpole", n, C.byref(cfg(**kw)))

@@ -51,12 +51,16 @@ def test_one_minibatch(mg, orc, env, n, T, B, block, layers, scale):
     check_minibatch(model, orc, d, orc.hparams(), p0, block_rows(s, n, B, block), B)
 
 
-@pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "cartpole_continuous_clamp", "voxelnav16",
-                                 "voxelnav"])
-def test_train_epochs(mg, orc, env):
-    """train(2) over 2 slots x 2 blocks: the block order and every minibatch's
-    LossStats match the oracle's train loop; weights stay within 1e-3."""
-    n, T, B = 1024, 2, 512
+@pytest.mark.parametrize("env,n,B", [(e, 1024, 512) for e in ("cartpole", "cartpole_continuous",
+                                                                 "cartpole_continuous_clamp", "voxelnav16", "voxelnav")]
+                         + [("cartpole", 8192, 4096), ("cartpole_continuous", 8192, 4096)])  # the benchmark minibatch
+def test_train_epochs(mg, orc, env, n, B):
+    """train(2) over 2 slots x n / B blocks (8 Adam steps): the block order and
+    every minibatch's LossStats match the oracle's train loop; weights stay
+    within 1e-3. At B = 4096 each step runs the benchmark's minibatch shape
+    (256 row tiles, 256 weight-gradient tiles) on rows the earlier steps'
+    weights produced."""
+    T = 2
     eid, _ = ENVS[env]
     gym, model, d = setup(mg, orc, env, n, T, B, seed=7)
     s = model.download_slots()

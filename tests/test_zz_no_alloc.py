@@ -4,8 +4,10 @@ mg_ppo_train_block on identical models: two calls in a row, the second with a
 smaller minibatch (and the Gaussian head, whose tile partials include the
 arena padding after log_std), so the second runs on the array the first left
 behind. Both run the same kernels on the same inputs, so parameters, Adam
-moments, the recomputed head and the LossStats must agree bit for bit. A
-policy whose workspace exceeds the array is rejected before any launch."""
+moments, the recomputed head and the LossStats must agree bit for bit, and the
+no-alloc model ends without a train workspace of its own (its captures query
+still reports that none was bound). A policy whose workspace exceeds the array
+is rejected before any launch."""
 import numpy as np
 import pytest
 
@@ -26,6 +28,8 @@ def twin_models(mg, env, n, B, seed, scale=4):
 
 
 def test_noalloc_matches_train_block(mg):
+    from metalgym_amd._capi import CapiError
+
     for env, n, B, block, seed in (("cartpole", 4096, 4096, 1, 3), ("cartpole_continuous", 1024, 512, 2, 5)):
         print(f"case {env} n={n} B={B} block={block}", flush=True)
         (_, ref), (gym, na) = twin_models(mg, env, n, B, seed)
@@ -48,6 +52,10 @@ def test_noalloc_matches_train_block(mg):
         ref.train_block(block)
         gym.sync()
         assert_bit_exact(na.params(), ref.params(), f"{env} parameters after a second step")
+        # the no-alloc model never bound a workspace of its own: nothing was allocated
+        with pytest.raises(CapiError) as e:
+            na.train_capture(0)
+        assert e.value.rc == -5, e.value
 
 
 def test_noalloc_rejects_a_workspace_beyond_the_array(mg):
