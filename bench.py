@@ -66,9 +66,18 @@ def bench_collect(kernel, n, T, steps, warmup, O, A, precision="fp32", layers=L)
     return gym, model, dt, times
 
 
+def rollout_bytes(gym, n, T):
+    """HBM bytes of one random rollout launch that no layout avoids: the T
+    slots (obs, action, reward, done) and each env's state, rng and done read
+    and written once. CartPole: 26.5 B per env-step. VoxelNav16: 129 B of
+    slots per env-step, its 4128-byte state once in and out per launch."""
+    slot = 4 * gym.obs_dim + gym.action_bytes + 4 + 1
+    return n * T * slot + n * 2 * (gym.state_bytes + 4 + 1)
+
+
 def bench_random(n, T, reps, kernel="rollout_cartpole", hbm=True):
-    """Random-policy rollouts; the HBM figures are CartPole's slot and state
-    bytes (26.5 B per env-step)."""
+    """Random-policy rollouts, with the launch's unavoidable HBM bytes
+    (rollout_bytes) over the kernel's event-timed duration."""
     import metalgym_amd as mg
 
     gym = mg.Gym(kernel, n, 0)
@@ -86,13 +95,40 @@ def bench_random(n, T, reps, kernel="rollout_cartpole", hbm=True):
     kms = kernel_avg_ms(times, "rollout")
     out = {"env_steps_per_s": reps * n * T / dt, "kernel_us": kms * 1e3}
     if hbm:
-        bytes_launch = n * T * 25 + n * 2 * (20 + 4 + 1)
+        bytes_launch = rollout_bytes(gym, n, T)
+        out["bytes_per_launch"] = bytes_launch
         out["hbm_GBps"] = bytes_launch / (kms * 1e-3) / 1e9
         out["hbm_frac"] = bytes_launch / (kms * 1e-3) / PEAK_HBM
     return out
 
 
-def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32", layers=L):
+def copy_floor_us(nbytes, reps=20):
+    """Device-to-device copies moving nbytes of HBM traffic (nbytes / 2 read,
+    nbytes / 2 written), each between regions no earlier copy touched, timed
+    with HIP events by the library (mg_memcpy_d2d); the median in us. The size
+    floor of a kernel with that much traffic (Adam's 28 B per parameter)."""
+    import metalgym_amd as mg
+
+    half = (nbytes // 2 + 255) // 256 * 256
+    src, dst = mg.DeviceBuffer(reps * half), mg.DeviceBuffer(reps * half)
+    src.zero()
+    dst.zero()
+    times = []
+    for k in range(reps):
+        mg.timing_reset()
+        mg.timing_enable(True)
+        mg.lib().mg_memcpy_d2d(dst.ptr + k * half, src.ptr + k * half, half)
+        mg.timing_enable(False)
+        tot, cnt = mg.timing_get()["copy"]
+        times.append(tot / cnt * 1e3)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32", layers=L, floor=False):
+    """The full loop (collect + train(epochs)), iters iterations untimed by
+    events, then one iteration with per-kernel HIP events. floor: also time a
+    device copy of Adam's byte count (copy_floor_us) in the same process."""
     import metalgym_amd as mg
 
     gym = mg.Gym(kernel, n, 0)
@@ -133,18 +169,35 @@ def bench_full(kernel, n, T, iters, O, A, epochs=4, precision="fp32", layers=L):
     kern["train_rows_TFLOPs"] = round(B * (fw + bw - fw) / tr / 1e12, 2)
     kern["train_dw_TFLOPs"] = round(B * fw / dw / 1e12, 2)
     kern["adam_GBps"] = round(count * 28 / ad / 1e9, 1)
+    if floor:
+        fl = copy_floor_us(count * 28)
+        kern["adam_copy_floor_us"] = round(fl, 2)
+        kern["adam_over_copy_floor"] = round(ad * 1e6 / fl, 2)
     out["kernels"] = kern
     return out
+
+
+def host_cores():
+    """The host's logical CPUs, and those this process may run on."""
+    cores = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = cores
+    return cores, usable
+
+
+def cpu_threads():
+    """Oracle threads: the usable host CPUs, at most 16 (a GPU box's CPU share)."""
+    return max(1, min(16, host_cores()[1]))
 
 
 def cpu_baseline(target_s=10.0):
     """The CPU oracle's collect() on a bounded slice of the headline workload
     (CartPole, T = 32, same network), on the host's cores."""
-    import numpy as np
-
     import oracle as orc
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     T = 32
     d = orc.dims(orc.CARTPOLE)
     params = orc.init_params(d, 0)
@@ -160,22 +213,36 @@ def cpu_baseline(target_s=10.0):
     dt = run(n)
     n = int(max(64, min(262144, n * target_s / max(dt, 1e-3))) // 64 * 64)
     dt = run(n)
+    cores, usable = host_cores()
     return {"value": n * T / dt, "unit": "env steps/s", "cores": threads, "kind": "port",
+            "host_cores": cores, "usable_cores": usable,
             "sample": f"oracle collect() of {n} of the 262144 CartPole envs, T=32, 2-block MLP, fp32, "
                       f"{threads} threads, {dt:.1f} s"}
 
 
 def cpu_extras(threads=None):
-    """The oracle on the host for the other benchmark configurations, bounded:
-    the random rollout at 262144 envs (config 1), and the full PPO loop at 4096
-    envs (config 3) from one collect and a few timed minibatches, an iteration
-    being one collect plus 4 epochs x 32 minibatches of 4096 rows."""
+    """The oracle on the host for every benchmark configuration, each bounded to
+    a few seconds and labelled with its scope (T = 32, the 2-block MLP, 4096-row
+    minibatches, 4 epochs; an iteration is one collect of all n envs plus
+    4 n T / 4096 minibatches):
+      config 1  random rollouts of 4096 and 262144 CartPole envs (whole launches);
+      config 2  collect() of 4096 CartPole envs (whole; 262144 is the headline
+                cpu_baseline's slice);
+      config 3  the full loop at 4096 envs (one whole collect, a few timed
+                minibatches) and at 262144 envs (scoped: a collect of a slice
+                of the envs and a few timed minibatches, combined at the
+                measured per-env-step and per-minibatch costs);
+      config 4  CartPoleContinuous full loop at 65536 and 262144 envs (scoped
+                the same way, one measurement for both sizes);
+      config 5  VoxelNav16 collect and full loop at 262144 envs (scoped).
+    Every entry states its threads, the host's cores and its scope."""
     import numpy as np
 
     import oracle as orc
 
-    threads = threads or max(1, min(16, os.cpu_count() or 1))
-    T = 32
+    threads = threads or cpu_threads()
+    cores, usable = host_cores()
+    T, B, epochs = 32, 4096, 4
     out = {}
 
     def repeated(fn, min_s=2.0):
@@ -188,32 +255,65 @@ def cpu_extras(threads=None):
             if dt >= min_s:
                 return calls, dt
 
-    n = 262144
-    g = orc.GymState(orc.CARTPOLE, n, 0)
-    reps, dt = repeated(lambda _: orc.rollout(g, T, random=True, threads=threads))
-    out["cpu_random_262144"] = {"env_steps_per_s": reps * n * T / dt, "cores": threads, "kind": "port",
-                                "sample": f"oracle random rollouts of 262144 CartPole envs x 32, {reps} in {dt:.1f} s"}
-    n = 4096
-    d = orc.dims(orc.CARTPOLE)
-    params = orc.init_params(d, 0)
-    g = orc.GymState(orc.CARTPOLE, n, 0)
-    slots = orc.Slots(orc.CARTPOLE, n, T)
-    nc, dc = repeated(lambda c: orc.collect(g, d, params, T, slots, first=(c == 0), threads=threads))
-    tc = dc / nc
-    hp = orc.hparams()
-    P, M, V = params.copy(), np.zeros_like(params), np.zeros_like(params)
+    def entry(value, scope, **kw):
+        e = {"env_steps_per_s": value, "cores": threads, "threads": threads, "host_cores": cores,
+             "usable_cores": usable, "kind": "port", "scope": scope}
+        e.update(kw)
+        return e
 
-    def minibatch(c):
-        t = c % T
-        orc.train_minibatch(d, hp, P, M, V, c + 1, slots.obs[t], slots.actions[t], slots.adv[t], slots.ret[t],
-                            slots.logp[t], threads=threads)
+    for n in (4096, 262144):  # config 1
+        g = orc.GymState(orc.CARTPOLE, n, 0)
+        reps, dt = repeated(lambda _: orc.rollout(g, T, random=True, threads=threads))
+        out[f"cpu_random_{n}"] = entry(reps * n * T / dt, f"{reps} whole random rollouts of {n} CartPole envs x 32 "
+                                                          f"in {dt:.1f} s")
 
-    k, dm = repeated(minibatch)
-    tm = dm / k
-    it = tc + 4 * T * tm
-    out["cpu_full_ppo_4096"] = {"env_steps_per_s": n * T / it, "cores": threads, "kind": "port",
-                                "sample": f"oracle collect of 4096 envs x 32 ({nc} in {dc:.1f} s) and {k} minibatches "
-                                          f"of 4096 rows ({tm:.2f} s each); iteration = collect + 128 minibatches"}
+    def collect_and_minibatches(env, n_collect, min_mb):
+        """Collect of n_collect envs (repeated for 2 s) and min_mb timed
+        minibatches of B rows of its slots; returns seconds per env-step of
+        collect, seconds per minibatch and the counts."""
+        d = orc.dims(env)
+        params = orc.init_params(d, 0)
+        g = orc.GymState(env, n_collect, 0)
+        slots = orc.Slots(env, n_collect, T)
+        nc, dc = repeated(lambda c: orc.collect(g, d, params, T, slots, first=(c == 0), threads=threads))
+        hp = orc.hparams()
+        P, M, V = params.copy(), np.zeros_like(params), np.zeros_like(params)
+
+        def minibatch(c):
+            t = c % T
+            rows = slice(0, B)
+            orc.train_minibatch(d, hp, P, M, V, c + 1, slots.obs[t, rows], slots.actions[t, rows],
+                                slots.adv[t, rows], slots.ret[t, rows], slots.logp[t, rows], threads=threads)
+
+        t0 = time.perf_counter()
+        for c in range(min_mb):
+            minibatch(c)
+        dm = time.perf_counter() - t0
+        return dc / (nc * n_collect * T), dm / min_mb, nc, min_mb
+
+    # config 2 at 4096 and config 3 at 4096: whole collects, timed minibatches
+    sc, sm, nc, k = collect_and_minibatches(orc.CARTPOLE, 4096, 4)
+    out["cpu_collect_4096"] = entry(1.0 / sc, f"{nc} whole collects of 4096 CartPole envs x 32")
+    it = 4096 * T * sc + epochs * (4096 * T // B) * sm
+    out["cpu_full_ppo_4096"] = entry(4096 * T / it, f"{nc} whole collects of 4096 envs x 32 and {k} minibatches of "
+                                                    f"4096 rows ({sm:.2f} s each); iteration = collect + 128 "
+                                                    f"minibatches", s_per_minibatch=sm)
+    # the 262144-env loops, scoped: a 16384-env collect slice and a few minibatches
+    for key, env, sizes in (("cpu_full_ppo", orc.CARTPOLE, (262144,)),
+                            ("cpu_continuous_full_ppo", orc.CARTPOLE_CONT, (65536, 262144)),
+                            ("cpu_voxelnav16_full_ppo", orc.VOXELNAV16, (262144,))):
+        sc, sm, nc, k = collect_and_minibatches(env, 16384, 3)
+        for n in sizes:
+            mbs = epochs * (n * T // B)
+            it = n * T * sc + mbs * sm
+            out[f"{key}_{n}"] = entry(n * T / it, f"scoped: {nc} collects of 16384 of the {n} envs x 32 "
+                                                  f"({sc * 1e9:.0f} ns per env-step) and {k} minibatches of 4096 rows "
+                                                  f"({sm:.2f} s each); iteration = {n} x 32 env-steps of collect + "
+                                                  f"{mbs} minibatches at those costs",
+                                      s_per_minibatch=sm, collect_env_steps_per_s=1.0 / sc)
+        if env == orc.VOXELNAV16:
+            out["cpu_voxelnav16_collect_262144"] = entry(1.0 / sc, f"scoped: {nc} collects of 16384 of the 262144 "
+                                                                   f"VoxelNav16 envs x 32")
     return out
 
 
@@ -234,10 +334,40 @@ def profile_pass(which):
     ("all" adds 64 copies of the Adam step's byte count, its size floor).
     "bf16": the collect and the minibatches in bf16 mode, and the copy.
     "train": one collect and two train(1) epochs of the 262144-env fp32 loop
-    (2048 minibatches each, enqueued back to back as in the benchmark)."""
+    (2048 minibatches each, enqueued back to back as in the benchmark).
+    "cfg45": configs 4 and 5 at 262144 envs: three collects and 64 minibatches
+    each of CartPoleContinuous and VoxelNav16, six VoxelNav16 random rollouts,
+    and the 1 GiB copy."""
     import metalgym_amd as mg
 
     n, T = 262144, 32
+    if which == "cfg45":  # configs 4 and 5: the continuous and VoxelNav16 kernels
+        for kernel in ("rollout_cartpole_continuous", "rollout_voxelnav16"):
+            gym = mg.Gym(kernel, n, 0)
+            model = mg.PPOModel(gym, horizon=T)
+            for _ in range(3):
+                model.collect()
+            sync()
+            print(f"profile: 3 collects of {kernel} at 262144 x 32", flush=True)
+            for b in range(64):
+                mg.lib().mg_ppo_train_block(model.h, b)
+            sync()
+            print(f"profile: 64 train minibatches of 4096 rows of {kernel}", flush=True)
+            del model, gym
+        gym = mg.Gym("rollout_voxelnav16", n, 0)
+        bufs = gym.rollout_random(T)
+        for _ in range(5):
+            gym.rollout_random(T, bufs, sync=False)
+        sync()
+        print("profile: 6 random rollouts of rollout_voxelnav16 at 262144 x 32", flush=True)
+        del gym, bufs
+        nbytes = 1 << 30
+        a, b = mg.DeviceBuffer(nbytes), mg.DeviceBuffer(nbytes)
+        a.zero()
+        mg.lib().mg_memcpy_d2d(b.ptr, a.ptr, nbytes)
+        sync()
+        print(f"profile: one device copy of {nbytes} bytes", flush=True)
+        return
     if which == "train":
         gym = mg.Gym("rollout_cartpole", n, 0)
         model = mg.PPOModel(gym, horizon=T)
@@ -301,7 +431,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--profile", choices=["collect", "random", "copy", "all", "bf16", "train"], default=None,
+    ap.add_argument("--profile", choices=["collect", "random", "copy", "all", "bf16", "train", "cfg45"], default=None,
                     help="run short kernel passes for rocprofv3 instead of the benchmark")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -339,7 +469,10 @@ def main():
                    "layers": L, "head": "softmax(2)+value", "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "kernel": "collect_kernel<CartPole,64,false,false>", "achieved": achieved / 1e12,
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
-                     "traffic": pmc_traffic(), "flop_per_launch": flop_launch, "kernel_ms": kms},
+                     "traffic": pmc_traffic(),
+                     "traffic_source": "profiles/collect_cartpole_262144_pmc.json: rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE of this kernel (a committed profile, not measured in this run)",
+                     "flop_per_launch": flop_launch, "kernel_ms": kms},
         "gae": {"kernel_us": gae_ms * 1e3, "hbm_GBps": (n * T * 17 + n * 4) / (gae_ms * 1e-3) / 1e9},
     }
     del model, gym
@@ -352,7 +485,7 @@ def main():
                                  "vs_published_m4_3.8M": 20 * 4096 * 32 / dt4 / 3.8e6}
         extra["full_ppo_4096"] = bench_full("rollout_cartpole", 4096, 32, 5, O, A)
         extra["full_ppo_4096"]["vs_published_m4_296K"] = extra["full_ppo_4096"]["env_steps_per_s"] / 296e3
-        extra["full_ppo_262144"] = bench_full("rollout_cartpole", 262144, 32, 1, O, A)
+        extra["full_ppo_262144"] = bench_full("rollout_cartpole", 262144, 32, 1, O, A, floor=True)
         # the README's 1-block rows (published Apple M4 figures: 6.7 M collect, 496 K full loop)
         _, _, dt1, _ = bench_collect("rollout_cartpole", 4096, 32, 20, 2, O, A, layers=1)
         extra["collect_4096_1block"] = {"env_steps_per_s": 20 * 4096 * 32 / dt1,
@@ -360,13 +493,17 @@ def main():
         extra["full_ppo_4096_1block"] = bench_full("rollout_cartpole", 4096, 32, 5, O, A, layers=1)
         extra["full_ppo_4096_1block"]["vs_published_m4_496K"] = \
             extra["full_ppo_4096_1block"]["env_steps_per_s"] / 496e3
-        _, _, dtc, _ = bench_collect("rollout_cartpole_continuous", 262144, 32, 3, 1, 4, 1)
-        extra["continuous_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtc}
+        _, _, dtc, tc = bench_collect("rollout_cartpole_continuous", 262144, 32, 3, 1, 4, 1)
+        kc = kernel_avg_ms(tc, "collect")
+        extra["continuous_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtc, "collect_ms": kc,
+                                              "mfma_frac": 33 * 262144 * fwd_flop(4, 1) / (kc * 1e-3) / PEAK_FP32_MFMA}
         extra["continuous_full_ppo_65536"] = bench_full("rollout_cartpole_continuous", 65536, 32, 2, 4, 1)
         extra["continuous_full_ppo_262144"] = bench_full("rollout_cartpole_continuous", 262144, 32, 1, 4, 1)
         _, _, dtv, tv = bench_collect("rollout_voxelnav16", 262144, 32, 3, 1, 30, 6)
-        extra["voxelnav16_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtv,
-                                              "collect_ms": kernel_avg_ms(tv, "collect")}
+        kv = kernel_avg_ms(tv, "collect")
+        extra["voxelnav16_collect_262144"] = {"env_steps_per_s": 3 * 262144 * 32 / dtv, "collect_ms": kv,
+                                              "mfma_frac": 33 * 262144 * fwd_flop(30, 6) / (kv * 1e-3) / PEAK_FP32_MFMA}
+        extra["voxelnav16_random_262144"] = bench_random(262144, 32, 10, "rollout_voxelnav16")
         extra["voxelnav16_full_ppo_262144"] = bench_full("rollout_voxelnav16", 262144, 32, 1, 30, 6)
         # the reference's heightmap VoxelNav at its README configuration (4096 envs,
         # 2-block policy; published Apple M4 figures: 7.9 M, 2.4 M, 265 K)

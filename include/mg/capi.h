@@ -396,7 +396,8 @@ enum {
     MG_K_GRAD_REDUCE = 6,
     MG_K_ADAM = 7,
     MG_K_FORWARD = 8,
-    MG_K_COUNT = 9
+    MG_K_COPY = 9, /* mg_memcpy_d2d: the size floor of a kernel's HBM traffic */
+    MG_K_COUNT = 10
 };
 typedef struct mg_kernel_times {
     double total_ms[MG_K_COUNT];

@@ -11,7 +11,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libmetalgym_amd.so")
 
 MAX_LAYERS = 8
-K_NAMES = ["rollout", "collect", "gae", "adv_stats", "train_rows", "train_dw", "grad_reduce", "adam", "forward"]
+K_NAMES = ["rollout", "collect", "gae", "adv_stats", "train_rows", "train_dw", "grad_reduce", "adam", "forward",
+           "copy"]
 
 
 class CapiError(RuntimeError):
@@ -82,7 +83,7 @@ class PPOSlots(C.Structure):
 
 
 class KernelTimes(C.Structure):
-    _fields_ = [("total_ms", C.c_double * 9), ("launches", C.c_uint64 * 9)]
+    _fields_ = [("total_ms", C.c_double * len(K_NAMES)), ("launches", C.c_uint64 * len(K_NAMES))]
 
     def as_dict(self):
         return {k: (self.total_ms[i], int(self.launches[i])) for i, k in enumerate(K_NAMES)}

@@ -158,7 +158,11 @@ int mg_memcpy_d2h(void* dst, const void* src, size_t bytes) {
     return MG_OK;
 }
 int mg_memcpy_d2d(void* dst, const void* src, size_t bytes) {
-    MG_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice), "hipMemcpy D2D");
+    {
+        TimedLaunch tl(MG_K_COPY, nullptr);
+        MG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, nullptr), "hipMemcpyAsync D2D");
+    }
+    MG_HIP(hipStreamSynchronize(nullptr), "hipMemcpy D2D synchronize");
     return MG_OK;
 }
 int mg_memset(void* dst, int value, size_t bytes) {
