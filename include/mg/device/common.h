@@ -89,6 +89,35 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// group_sum of each of N values, the steps of all N interleaved (the same
+// bits per value as group_sum).
+template <int G, int N>
+__device__ __forceinline__ void group_sum_n(float (&v)[N]) {
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "power-of-two group");
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if constexpr (G >= 2) v[i] += dpp_lane<0xB1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if constexpr (G >= 4) v[i] += dpp_lane<0x4E>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if constexpr (G >= 8) v[i] += dpp_lane<0x141>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if constexpr (G >= 16) v[i] += dpp_lane<0x140>(v[i]);
+    if constexpr (G >= 32) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const float lo = lane_value<0>(v[i]) + lane_value<16>(v[i]), hi = lane_value<32>(v[i]) + lane_value<48>(v[i]);
+            if constexpr (G == 32)
+                v[i] = (threadIdx.x & 32) ? hi : lo;
+            else
+                v[i] = lo + hi;
+        }
+    }
+}
+
 // Sum of t[0..N) as a pairwise tree (t[c] + t[c + N/2], then halves again),
 // five dependent adds for 32 terms instead of 31; N a power of two. Overwrites t.
 template <int N>

@@ -34,11 +34,12 @@ struct alignas(16) SkSmem {
     float red[W][kTR * kLds];    // the waves' partials of a block output; W_in / b_in at start-up
     float part[kTR][2][kEmbed];  // per row: xn dZ and dZ of the last LN backward (dgamma, dbeta terms)
     float xn[(Sh::LAYERS + 1) * kTR * kEmbed];  // LN captures for the backward
-    float sd[(Sh::LAYERS + 1) * kTR];
+    float rstd[(Sh::LAYERS + 1) * kTR];  // 1 / sigma of every LN
     float ln[(Sh::LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
     float wh[kEmbed * Sh::HEAD];              // W_head
     float obs[kTR * Sh::OBS];
-    float head[kTR * Sh::HEAD];
+    float acts[kTR * Sh::HEAD];  // the tile's float actions (Gaussian head)
+    float lstd[Sh::HEAD];        // log_std (Gaussian head)
     float dhead[kTR * Sh::HEAD];
     float dls[kTR * Sh::HEAD];
     float stat[kTR * 5];
@@ -75,11 +76,37 @@ __device__ __forceinline__ RowVec<SkShape<W>::NV> sk_layernorm_bwd(SkSmem<W>& L,
     rv_store(&L.part[row][1][c0], g);
     s1 = group_sum<TPR>(s1);
     s2 = group_sum<TPR>(s2);
-    const float r1 = s1 / (float)kEmbed, r2 = s2 / (float)kEmbed, rd = 1.0f / L.sd[lnIdx * kTR + row];
+    const float r1 = s1 / (float)kEmbed, r2 = s2 / (float)kEmbed, rd = L.rstd[lnIdx * kTR + row];
     RowVec<NV> o;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) o[c] = rd * (dxn[c] - r1 - xv[c] * r2);
     return o;
+}
+
+// model/layernorm.metal:10-71 on a row held by TPR lanes, returning 1 / sigma
+// (one v_rsq_f32, about 1 ulp) for the backward instead of sigma.
+template <int TPR, int NV>
+__device__ __forceinline__ void sk_layernorm_r(const RowVec<NV>& h, const float* gamma, const float* beta, int c0,
+                                               RowVec<NV>& x, RowVec<NV>& xn, float& rstd) {
+    constexpr int CPT = 4 * NV;
+    float s = h[0];
+#pragma unroll
+    for (int c = 1; c < CPT; ++c) s += h[c];
+    s = group_sum<TPR>(s);
+    const float mean = s * (1.0f / (float)kEmbed);
+    float q = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const float d = h[c] - mean;
+        q += d * d;
+    }
+    q = group_sum<TPR>(q);
+    rstd = __builtin_amdgcn_rsqf(q * (1.0f / (float)kEmbed) + 1e-5f);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        xn[c] = (h[c] - mean) * rstd;
+        x[c] = gamma[c0 + c] * xn[c] + beta[c0 + c];
+    }
 }
 
 // The tile's dgamma and dbeta (rows summed in order) from part; after a
@@ -96,7 +123,107 @@ __device__ __forceinline__ void sk_ln_sums(const SkSmem<W>& L, float* tp_gamma, 
     }
 }
 
-template <int W>
+// model/linear.metal:17-37 for one row held by TPR lanes: hv[j] = x_f[row] .
+// W_head[:, j] for j < HD (0 for HD <= j < HC), the HC column sums reduced
+// together, so every lane of the row holds the whole head. wh: W_head in LDS.
+template <int TPR, int HC, int NV>
+__device__ __forceinline__ void sk_head(const RowVec<NV>& x, const float* wh, int HD, int c0, float (&hv)[HC]) {
+    constexpr int CPT = 4 * NV;
+#pragma unroll
+    for (int j = 0; j < HC; ++j) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const float w = wh[(c0 + c) * HD + j];  // in the LDS array for every j < HC
+            acc += x[c] * (j < HD ? w : 0.0f);
+        }
+        hv[j] = acc;
+    }
+    group_sum_n<TPR, HC>(hv);
+}
+
+// model/policy.metal:14-69 / model/gaussian.metal:76-135 for one row from its
+// whole head hv (A actions, HD = A + 1 <= HC columns), computed by every lane
+// of the row alike: the head gradient dz[j] (0 from HD on), the Gaussian
+// head's log_std gradients dls[j] (j < A) and the row's LossStats terms st.
+// Sums over the head columns run in column order. lstd: log_std, actRow: the
+// row's A float actions (both LDS, Gaussian head only); act: the discrete
+// action.
+template <int HC>
+__device__ __forceinline__ void sk_loss_row(const RowsArgs& a, const float (&hv)[HC], int A, bool cont,
+                                            const float* lstd, const float* actRow, float an, float oldLp, float ret,
+                                            int act, float (&dz)[HC], float (&dls)[HC], float (&st)[5]) {
+    const float scale = 1.0f / (float)a.step.rows;
+    const float clip = a.hp.clip, ec = a.hp.entropy_coef;
+    float entropy = 0.0f, logpA = 0.0f, value = 0.0f;
+    float pr[HC], lp[HC], is[HC], dd[HC];
+#pragma unroll
+    for (int j = 0; j < HC; ++j) {
+        pr[j] = lp[j] = is[j] = dd[j] = 0.0f;
+        value = j == A ? hv[j] : value;
+    }
+    if (!cont) {  // model/policy.metal:14-69
+        float zmax = -__builtin_huge_valf();
+#pragma unroll
+        for (int j = 0; j < HC; ++j) zmax = j < A ? fmaxf(zmax, hv[j]) : zmax;
+        float e = 0.0f;
+#pragma unroll
+        for (int j = 0; j < HC; ++j)
+            if (j < A) e += fast_exp(hv[j] - zmax);
+        const float lse = zmax + fast_log(e);
+        float za = 0.0f;
+#pragma unroll
+        for (int j = 0; j < HC; ++j) {
+            if (j < A) {
+                lp[j] = hv[j] - lse;
+                pr[j] = fast_exp(lp[j]);
+                entropy -= pr[j] * lp[j];
+            }
+            za = j == act ? hv[j] : za;
+        }
+        logpA = za - lse;
+    } else {  // model/gaussian.metal:76-135
+#pragma unroll
+        for (int j = 0; j < HC; ++j) {
+            if (j < A) {
+                const float ls = lstd[j];
+                is[j] = fast_exp(-ls);
+                dd[j] = (actRow[j] - hv[j]) * is[j];
+                logpA += -0.5f * dd[j] * dd[j] - ls - kLogSqrt2Pi;
+                entropy += ls + kLogSqrt2Pi + 0.5f;
+            }
+        }
+    }
+    const float ratio = fast_exp(logpA - oldLp);
+    const float surr1 = ratio * an;
+    const float cr = fminf(fmaxf(ratio, 1.0f - clip), 1.0f + clip);
+    const float surr2 = cr * an;
+    const float gLogp = (surr1 <= surr2) ? -an * ratio : 0.0f;
+    const float vErr = value - ret;
+#pragma unroll
+    for (int j = 0; j < HC; ++j) {
+        float d = 0.0f, l = 0.0f;
+        if (j < A) {
+            if (!cont) {
+                d = (gLogp * ((j == act ? 1.0f : 0.0f) - pr[j]) + ec * pr[j] * (lp[j] + entropy)) * scale;
+            } else {
+                d = gLogp * dd[j] * is[j] * scale;
+                l = (gLogp * (dd[j] * dd[j] - 1.0f) - ec) * scale;
+            }
+        }
+        dz[j] = j == A ? a.hp.value_coef * vErr * scale : d;
+        dls[j] = l;
+    }
+    st[0] = -(surr1 < surr2 ? surr1 : surr2);
+    st[1] = 0.5f * a.hp.value_coef * vErr * vErr;
+    st[2] = entropy;
+    st[3] = oldLp - logpA;
+    st[4] = (fabsf(ratio - 1.0f) > clip) ? 1.0f : 0.0f;
+}
+
+// HC: a compile-time bound on the head width (4, 8 or 16), for the head and
+// loss in registers.
+template <int W, int HC>
 __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs a) {
     using Sh = SkShape<W>;
     constexpr int M = kTR, NT = Sh::NT, S = Sh::S, TPR = Sh::TPR, CPT = Sh::CPT, NV = Sh::NV;
@@ -163,6 +290,12 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     for (int idx = tid + NT; idx < n_wh; idx += NT) L.wh[idx] = pv.params[pv.off_head + idx];
 #pragma unroll 4
     for (int idx = tid + 2 * NT; idx < n_ln; idx += NT) L.ln[idx] = lnp[idx];
+    const int A = (int)pv.act_dim;
+    if (pv.continuous) {  // the Gaussian head's inputs of the loss
+        const float* af = static_cast<const float*>(a.action_slots) + g0 * A;
+        if (tid < M * A) L.acts[tid] = af[tid];
+        if (tid < A) L.lstd[tid] = pv.params[pv.off_log_std + tid];
+    }
     float an, oldLp, ret;
     int act = 0;
     {
@@ -191,10 +324,10 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     }
     for (int l = 0; l < NL; ++l) {
         RowVec<NV> x, xn;
-        float sd;
-        sk_layernorm<TPR>(h, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, c0, x, xn, sd);
+        float sd;  // 1 / sigma
+        sk_layernorm_r<TPR>(h, L.ln + l * 2 * kEmbed, L.ln + l * 2 * kEmbed + kEmbed, c0, x, xn, sd);
         rv_store(L.xn + (l * M + row) * kEmbed + c0, xn);
-        if (lk == 0) L.sd[l * M + row] = sd;
+        if (lk == 0) L.rstd[l * M + row] = sd;
         rv_store(cx + ((size_t)l * B + r0 + row) * kEmbed + c0, x);
         rv_store(L.xs + row * kLds + c0, x);
         __syncthreads();  // X complete; every wave is past its reads of red (and of W_in)
@@ -222,33 +355,55 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         }
         h = rv_add(h, sk_reduce<W>(L, hp, wave, row, c0));  // model/elementwise.metal:4-13
     }
-    {  // final LN; x_f also stays in xs for dW_head
+    // ---- final LN, head, loss and the head's backward, each row in its lanes'
+    // registers (model/ppo.h:616-625, then model/ppo.h:793-806) ----
+    RowVec<NV> D;
+    {
         RowVec<NV> x, xn;
-        float sd;
-        sk_layernorm<TPR>(h, L.ln + NL * 2 * kEmbed, L.ln + NL * 2 * kEmbed + kEmbed, c0, x, xn, sd);
+        float sd;  // 1 / sigma
+        sk_layernorm_r<TPR>(h, L.ln + NL * 2 * kEmbed, L.ln + NL * 2 * kEmbed + kEmbed, c0, x, xn, sd);
         rv_store(L.xn + (NL * M + row) * kEmbed + c0, xn);
-        if (lk == 0) L.sd[NL * M + row] = sd;
-        rv_store(L.xs + row * kLds + c0, x);
-        // model/linear.metal:17-37: head[row][j] = x_f[row] . W_head[:, j]
-        for (int j = 0; j < HD; ++j) {
-            float acc = 0.0f;
+        if (lk == 0) L.rstd[NL * M + row] = sd;
+        rv_store(L.xs + row * kLds + c0, x);  // x_f for dW_head
+        float hv[HC], dz[HC], dls[HC], st[5];
+        sk_head<TPR, HC>(x, L.wh, HD, c0, hv);
+        sk_loss_row<HC>(a, hv, A, pv.continuous != 0, L.lstd, L.acts + row * A, an, oldLp, ret, act, dz, dls, st);
+        // lane lk < HD of the row writes head column lk and its gradient
+        float hm = 0.0f, dm = 0.0f, lm = 0.0f;
 #pragma unroll
-            for (int c = 0; c < CPT; ++c) acc += x[c] * L.wh[(c0 + c) * HD + j];
-            acc = group_sum<TPR>(acc);
-            if (lk == 0) L.head[row * HD + j] = acc;
+        for (int j = 0; j < HC; ++j) {
+            hm = j == lk ? hv[j] : hm;
+            dm = j == lk ? dz[j] : dm;
+            lm = j == lk ? dls[j] : lm;
         }
+        if (lk < HD) {
+            L.dhead[row * HD + lk] = dm;
+            if (a.head_out) a.head_out[(size_t)(r0 + row) * HD + lk] = hm;
+        }
+        if (pv.continuous && lk < A) L.dls[row * A + lk] = lm;
+        if (lk == 0) {
+#pragma unroll
+            for (int q = 0; q < 5; ++q) L.stat[row * 5 + q] = st[q];
+        }
+        // model/linear.metal:40-60: the gradient at the final LN output, then its LN
+        RowVec<NV> g = rv_zero<NV>();
+#pragma unroll
+        for (int j = 0; j < HC; ++j)
+#pragma unroll
+            for (int c = 0; c < CPT; ++c) {
+                const float w = L.wh[(c0 + c) * HD + j];
+                g[c] += dz[j] * (j < HD ? w : 0.0f);
+            }
+        D = sk_layernorm_bwd<W>(L, g, NL, row, c0);
     }
-    __syncthreads();
-
-    loss_rows<TPR>(a, LossIo{L.head, L.dhead, L.dls, L.stat}, row, lk, an, oldLp, ret, act, r0, g0);
-    __syncthreads();
+    __syncthreads();  // dhead, dls, the LossStats terms and the LN's part terms written
 
     // model/linear.metal:71-93 on this tile: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
     tile_outer<M, NT>(L.dhead, HD, HD, L.xs, tp + pv.float_group, 1, HD);
     if (pv.continuous && tid < kEmbed) {  // model/gaussian.metal:166-168, summed over the tile in row order
         float s = 0.0f;
-        if (tid < (int)pv.act_dim)
-            for (int r = 0; r < M; ++r) s += L.dls[r * pv.act_dim + tid];
+        if (tid < A)
+            for (int r = 0; r < M; ++r) s += L.dls[r * A + tid];
         tp[pv.off_log_std + tid] = s;  // and 0 in the arena padding after log_std (A <= 63 < 128)
     }
     if (tid >= 64 && tid < 64 + 5) {  // the tile's LossStats sums, in row order
@@ -257,19 +412,8 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         for (int r = 0; r < M; ++r) s += L.stat[r * 5 + qq];
         tp[pv.float_group + kEmbed * HD + qq] = s;
     }
-
-    // ---- backward (model/ppo.h:793-865) ----
-    RowVec<NV> D;
-    {  // model/linear.metal:40-60: the gradient at the final LN output, then its LN
-        RowVec<NV> g = rv_zero<NV>();
-        for (int j = 0; j < HD; ++j) {
-            const float dz = L.dhead[row * HD + j];
-#pragma unroll
-            for (int c = 0; c < CPT; ++c) g[c] += dz * L.wh[(c0 + c) * HD + j];
-        }
-        D = sk_layernorm_bwd<W>(L, g, NL, row, c0);
-    }
     __syncthreads();  // dW_head's reads of x_f in xs are done before xs takes dh
+
     int lnDone = NL;  // the LN whose dgamma / dbeta terms are in part
     for (int l = NL - 1; l >= 0; --l) {  // model/mlp.metal:88-153 + model/ppo.h:851-852
         rv_store(cdh + ((size_t)l * B + r0 + row) * kEmbed + c0, D);

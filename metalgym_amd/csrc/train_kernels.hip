@@ -1016,9 +1016,14 @@ template <int NW, int U, int NB>
 __global__ void __launch_bounds__(64 * NW) train_dw_fused_kernel(const DwFusedArgs<float> a) {
     __shared__ float red[NW][32 * 32];
     float sq = 0.0f;
-    {
+    const uint32_t T = a.dw.big_tiles;  // workgroups [0, T): one 32 x 32 tile each
+    if (blockIdx.x >= T) {
+        // the tile-partial columns on workgroups of their own, which run beside
+        // the tile workgroups instead of after some of them
+        sq = reduce_tile_partials<64 * NW>(a.red, blockIdx.x - T, gridDim.x - T);
+    } else {
         const uint32_t per = a.dw.tiles_per_big[0];  // every matrix has E H / 1024 tiles
-        const uint32_t t = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+        const uint32_t t = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8;
         const uint32_t mi = t / per, eb = (t % per) % (kEmbed / 32), hb = (t % per) / (kEmbed / 32);
         const BigMatT<float>& bm = a.dw.big[mi];
         const bool up = bm.mdim == (uint32_t)kEmbed;  // up: X is the embed side
@@ -1065,8 +1070,8 @@ __global__ void __launch_bounds__(64 * NW) train_dw_fused_kernel(const DwFusedAr
             out[(size_t)(e >> 5) * bm.ndim + (e & 31)] = v;
             sq += v * v;
         }
+        if (gridDim.x == T) sq += reduce_tile_partials<64 * NW>(a.red, blockIdx.x, gridDim.x);
     }
-    sq += reduce_tile_partials<64 * NW>(a.red, blockIdx.x, gridDim.x);
     write_norm_part<NW>(sq, a.red.normpart + blockIdx.x);
     if (blockIdx.x == 0)
         for (uint32_t i = gridDim.x + threadIdx.x; i < (uint32_t)kReduceBlocks; i += 64 * NW) a.red.normpart[i] = 0.0f;
@@ -1383,6 +1388,17 @@ dev::DwArgsT<T> dw_args(const mg_policy_view& pv, const TrainWs& ws, uint32_t B,
     return da;
 }
 
+// The split row pass with the head width's compile-time bound.
+template <int W>
+void launch_rows_split(hipStream_t st, uint32_t B, const mg_policy_view& pv, const dev::RowsArgs& ra) {
+    if (pv.head_dim <= 4)
+        hipLaunchKernelGGL((dev::train_rows_split_kernel<W, 4>), dim3(B / dev::kTR), dim3(64 * W), 0, st, ra);
+    else if (pv.head_dim <= 8)
+        hipLaunchKernelGGL((dev::train_rows_split_kernel<W, 8>), dim3(B / dev::kTR), dim3(64 * W), 0, st, ra);
+    else
+        hipLaunchKernelGGL((dev::train_rows_split_kernel<W, 16>), dim3(B / dev::kTR), dim3(64 * W), 0, st, ra);
+}
+
 int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hparams& hp, float lr,
                       const TrainWs& ws, const TrainStep& step, const float* obs_slots, const void* action_slots,
                       const float* adv_slots, const float* ret_slots, const float* logp_slots,
@@ -1423,9 +1439,9 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         if (bf)
             hipLaunchKernelGGL(dev::train_rows_kernel<true>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         else if (dev::rows_split_waves(pv) == 8)
-            hipLaunchKernelGGL(dev::train_rows_split_kernel<8>, dim3(B / dev::kTR), dim3(64 * 8), 0, st, ra);
+            launch_rows_split<8>(st, B, pv, ra);
         else if (dev::rows_split_waves(pv) == 4)
-            hipLaunchKernelGGL(dev::train_rows_split_kernel<4>, dim3(B / dev::kTR), dim3(64 * 4), 0, st, ra);
+            launch_rows_split<4>(st, B, pv, ra);
         else
             hipLaunchKernelGGL(dev::train_rows_kernel<false>, dim3(B / dev::kTR), dim3(dev::kTNT), 0, st, ra);
         MG_HIP(hipGetLastError(), "train rows launch");
@@ -1465,7 +1481,10 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         dev::DwFusedArgs<float> fa;
         fa.dw = dw_args<float>(pv, ws, B, 1, 32);
         fa.red = ga;
-        hipLaunchKernelGGL((dev::train_dw_fused_kernel<dev::kDwf32Waves, dev::kDwf32U, dev::kDwf32Sets>), dim3(tiles32),
+        // the tile-partial columns on small_wgs extra workgroups where the
+        // partial norms have room for them, else on the first tile workgroups
+        const uint32_t grid = tiles32 + ga.small_wgs <= (uint32_t)kReduceBlocks ? tiles32 + ga.small_wgs : tiles32;
+        hipLaunchKernelGGL((dev::train_dw_fused_kernel<dev::kDwf32Waves, dev::kDwf32U, dev::kDwf32Sets>), dim3(grid),
                            dim3(64 * dev::kDwf32Waves), 0, st, fa);
         MG_HIP(hipGetLastError(), "train dW launch");
     } else {
