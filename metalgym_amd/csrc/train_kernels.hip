@@ -911,19 +911,19 @@ __global__ void __launch_bounds__(256) grad_reduce_kernel(const ReduceArgs a) {
 
 // bf16 weight gradients, tile partial sums and partial norms in one launch
 // (replacing train_dw + grad_reduce when the block matrices have enough 32 x
-// 32 tiles to fill the GPU without row splits). Workgroup t computes tile t
-// of the block matrices over all rows, operands as in train_dw_bf16_kernel:
-// its NW waves take every NW-th 16-row step and add their tiles in LDS in
-// wave order, and the tile goes straight to grad. Each wave keeps up to 2 U
-// steps of loads in flight. Then the workgroups share the tile-partial
+// 32 tiles to fill the GPU without row splits). Each of the first T
+// workgroups computes one tile of the block matrices over all rows, operands
+// as in train_dw_bf16_kernel: its NW waves take every NW-th 16-row step and
+// add their tiles in LDS in wave order, and the tile goes straight to grad.
+// Each wave keeps up to 2 U steps of loads in flight. The workgroups past T
+// (or, in a grid of T, the tile workgroups afterwards) share the tile-partial
 // columns (reduce_tile_partials). Every
 // workgroup writes the squared norm of what it wrote to normpart; the entries
 // past the grid are zeroed, so the Adam kernel's fixed-order sum over
 // kReduceBlocks entries is the same sum. (At 4096 rows, 2 blocks, hidden 512:
 // 16 waves with U = 4 or 2 and 8 waves with U = 4 ran within 3% of each other.
-// The kernel moves ≈50 MB between L2 and the fabric, more than the 20 MB of
-// captures: each XCD fetches the capture blocks its tiles share. Against the
-// split kernel plus grad_reduce it saves one launch per minibatch.)
+// Against the split kernel plus grad_reduce it saves one launch per
+// minibatch.)
 template <class T>
 struct DwFusedArgs {
     DwArgsT<T> dw;
@@ -933,17 +933,25 @@ template <int NW, int U>
 __global__ void __launch_bounds__(64 * NW) train_dw_bf16_fused_kernel(const DwFusedArgs<uint16_t> a) {
     __shared__ float red[NW][32 * 32];
     float sq = 0.0f;
-    {
-        uint32_t t = blockIdx.x, m = 0;
+    const uint32_t T = a.dw.big_tiles;  // workgroups [0, T): one 32 x 32 tile each
+    if (blockIdx.x >= T) {
+        // the tile-partial columns on workgroups of their own, as in train_dw_fused_kernel
+        sq = reduce_tile_partials<64 * NW>(a.red, blockIdx.x - T, gridDim.x - T);
+    } else {
+        // workgroups go to the 8 XCDs round robin, so workgroup b takes tile
+        // (b mod 8) T / 8 + b / 8 of the order (matrix, hidden block, embed
+        // block): an XCD's tiles are every embed block of a run of hidden
+        // blocks of one matrix (T = 256: 8 hidden blocks), so it fetches the
+        // matrix's embed-side capture once and half its hidden-side one (at
+        // 4096 rows, hidden 512, 2 blocks: 13.2 -> 12.3 us against the order
+        // with the hidden block fastest, whose XCDs each fetched the embed-side
+        // captures of all four matrices). T is a multiple of 8.
+        uint32_t t = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8, m = 0;
         while (t >= a.dw.tiles_per_big[m]) t -= a.dw.tiles_per_big[m], ++m;
         const BigMatT<uint16_t>& bm = a.dw.big[m];
-        // the hidden-side tile index varies fastest: workgroups go to the 8 XCDs
-        // round robin (and every matrix has a multiple of 8 tiles), so XCD k
-        // computes the tiles of hidden blocks k and k + 8 for every embed block
-        // and each capture block is fetched into its L2 by as few XCDs as can
         const uint32_t ntm = bm.mdim / 32, ntn = bm.ndim / 32;
-        const uint32_t tm = bm.mdim > bm.ndim ? t % ntm : t / ntn;
-        const uint32_t tn = bm.mdim > bm.ndim ? t / ntm : t % ntn;
+        const uint32_t tm = bm.mdim > bm.ndim ? t / ntn : t % ntm;
+        const uint32_t tn = bm.mdim > bm.ndim ? t % ntn : t / ntm;
         const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
         // lane's operands in step s: row group 2 (NW s + w) + lane / 32, column
         // tile + lane % 32
@@ -986,8 +994,8 @@ __global__ void __launch_bounds__(64 * NW) train_dw_bf16_fused_kernel(const DwFu
             out[(size_t)(e >> 5) * bm.ndim + (e & 31)] = v;
             sq += v * v;
         }
+        if (gridDim.x == T) sq += reduce_tile_partials<64 * NW>(a.red, blockIdx.x, gridDim.x);
     }
-    sq += reduce_tile_partials<64 * NW>(a.red, blockIdx.x, gridDim.x);
     write_norm_part<NW>(sq, a.red.normpart + blockIdx.x);
     if (blockIdx.x == 0)
         for (uint32_t i = gridDim.x + threadIdx.x; i < (uint32_t)kReduceBlocks; i += 64 * NW) a.red.normpart[i] = 0.0f;
@@ -1472,7 +1480,8 @@ int launch_train_step(hipStream_t st, const mg_policy_view& pv, const mg_ppo_hpa
         dev::DwFusedArgs<uint16_t> fa;
         fa.dw = dw_args<uint16_t>(pv, ws, B, 1, 32);
         fa.red = ga;
-        hipLaunchKernelGGL((dev::train_dw_bf16_fused_kernel<dev::kDwfWaves, 4>), dim3(tiles32),
+        const uint32_t grid = tiles32 + ga.small_wgs <= (uint32_t)kReduceBlocks ? tiles32 + ga.small_wgs : tiles32;
+        hipLaunchKernelGGL((dev::train_dw_bf16_fused_kernel<dev::kDwfWaves, 4>), dim3(grid),
                            dim3(64 * dev::kDwfWaves), 0, st, fa);
         MG_HIP(hipGetLastError(), "train dW launch");
     } else if (!bf && tiles32 >= 128 && tiles32 <= (uint32_t)kReduceBlocks &&
