@@ -46,16 +46,44 @@ using TSmemB = FwdSmemB<kTR, 2>;  // the same with bf16 GEMM operands
 
 // Per-tile outer-product sums in one pass: out[k * ks + c * cs] =
 // sum_r a[r * lda + k] * b[r * kLds + c] for k < K and the 128 columns c, rows
-// added in order by one thread per output. a and b are LDS tiles of M rows.
-// Thread t owns column t % 128 and the k = t / 128 + (NT / 128) j: its column
-// of b is read once into registers, and a wave's reads of a are broadcasts of
-// one address (VoxelNav16's 30 x 128 embed gradient: 240 LDS reads per thread
-// one output at a time, 3.2 K cycles of the row pass). No barrier (the caller
-// orders the inputs before and the outputs after).
+// added in order. a and b are LDS tiles of M = 16 rows. No barrier (the
+// caller orders the inputs before and the outputs after).
+//  - K < 16: one thread per output. Thread t owns column t % 128 and the
+//    k = t / 128 + (NT / 128) j: its column of b is read once into
+//    registers, and a wave's reads of a are broadcasts of one address.
+//  - K >= 16 (VoxelNav16's 30 x 128 embed gradient, 240 LDS reads per thread
+//    one output at a time): 16 x 16 output tiles on v_mfma_f32_16x16x4_f32,
+//    one per wave in turn, A = a^T (lane (q, m): a[4 s + q][16 kb + m], 0
+//    past K), B = b, four row steps; the same sums in the same order (rows
+//    in order, each added with an FMA). For K of 3 or 4 the MFMA tiles were
+//    0.5 us slower than one thread per output.
 template <int M, int NT>
 __device__ __forceinline__ void tile_outer(const float* a, int lda, int K, const float* b, float* out, int ks,
                                            int cs) {
     static_assert(NT % kEmbed == 0, "whole columns per pass");
+    static_assert(M == 16, "16-row tiles: four 16x16x4 row steps");
+    if (K >= 16) {
+        constexpr int NW = NT / 64;
+        const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+        const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const int tiles = 8 * ((K + 15) / 16);
+        for (int t = wave; t < tiles; t += NW) {
+            const int kb = t >> 3, c = 16 * (t & 7) + n, k = 16 * kb + n;
+            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int r = 4 * s + q;
+                const float av = k < K ? a[r * lda + k] : 0.0f;
+                acc = mfma16x16x4(av, b[r * kLds + c], acc);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kk = 16 * kb + 4 * q + i;
+                if (kk < K) out[kk * ks + c * cs] = acc[i];
+            }
+        }
+        return;
+    }
     const int c = threadIdx.x % kEmbed, k0 = threadIdx.x / kEmbed;
     if (k0 < K) {
         float bv[M];
