@@ -49,11 +49,37 @@ struct CollectFwd {
     using Smem = std::conditional_t<SPLIT, SplitFwdSmem<8>, std::conditional_t<BF16, FwdSmemB<M>, FwdSmem<M>>>;
 };
 
+// The tile's LDS: the forward's, then the staged observations and the head.
+// Outside the split forward the observations ([M][O]) and the head ([M][HD])
+// share the forward's hidden-chunk buffer: the observations are read only by
+// the embed, before the first chunk is written (LN0's barriers between), and
+// the head is written after the final LN's first barrier, when every wave is
+// done with the last chunk; the env phase that reads the head and writes the
+// next observations ends before the next forward. That leaves room at two
+// workgroups per CU for VoxelNav16's small parameters but W_in (SmallStage).
+// 16-byte aligned in size as well, so the dynamic LDS after the static
+// arrays (the staged small parameters, read as float4s) starts 16-byte
+// aligned: at 4 bytes past a 16-byte boundary the CartPole collect ran 8%
+// slower, bf16 41%.
 template <int M, int O, int HD, bool BF16>
-struct CollectSmem {
-    typename CollectFwd<M, O, BF16>::Smem fwd;
-    float obs[M * O];
-    float head[M * HD];
+struct alignas(16) CollectSmem {
+    using Fwd = typename CollectFwd<M, O, BF16>::Smem;
+    static constexpr size_t IO = (size_t)M * (O + HD);  // floats: obs, then head
+    static constexpr bool ALIAS = !CollectFwd<M, O, BF16>::SPLIT && IO * 4 <= (BF16 ? (size_t)M * kLdsB * 2
+                                                                                       : (size_t)M * kLds * 4);
+    Fwd fwd;
+    float io[ALIAS ? 1 : IO];
+    __device__ __forceinline__ float* obs() {
+        if constexpr (ALIAS) {
+            if constexpr (BF16)
+                return reinterpret_cast<float*>(&fwd.vb[0][0]);
+            else
+                return &fwd.vs[0][0];
+        } else {
+            return io;
+        }
+    }
+    __device__ __forceinline__ float* head() { return obs() + M * O; }
 };
 
 // LDS staging of a State too large for registers: the tile's M states at an
@@ -83,15 +109,18 @@ struct LdsState {
 // an L2 round trip (at one workgroup per CU no other workgroup's MFMAs overlap
 // that latency; at two, 64-row tiles, it took the 262144-env CartPole collect
 // from 36.0 to 35.4 ms). Used when they fit beside the kernel's static LDS at
-// its workgroups per CU; else the forward reads the arena. The launcher
-// decides from the static size the compiler gave the kernel (padding
-// included) and passes the decision as the kernel's second argument.
+// its workgroups per CU (kAll); else all but W_in where those fit (kNoWin:
+// W_in is read once per step, by the embed's MFMAs), else none and the forward
+// reads the arena. The launcher decides from the static size the compiler gave
+// the kernel (padding included) and passes the decision as the kernel's
+// second argument.
 template <typename Env, int M, bool BF16>
 struct SmallStage {
     static constexpr int O = Env::OBS_DIM, HD = Env::ACT_DIM + 1;
     static constexpr int WIN = O * kEmbed, BIN = kEmbed, WH = kEmbed * HD;
-    __host__ __device__ static constexpr uint32_t floats(uint32_t layers) {
-        return WIN + BIN + (layers + 1) * 2 * kEmbed + WH;
+    static constexpr uint32_t kNone = 0, kAll = 1, kNoWin = 2;
+    __host__ __device__ static constexpr uint32_t floats(uint32_t layers, uint32_t mode = kAll) {
+        return (mode == kAll ? WIN : 0) + BIN + (layers + 1) * 2 * kEmbed + WH;
     }
 };
 
@@ -120,7 +149,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     __shared__ CollectSmem<M, O, HD, BF16> sm;
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     using SS = SmallStage<Env, M, BF16>;
-    extern __shared__ float small_lds[];  // SS::floats(layers) floats when stage_small
+    extern __shared__ __align__(16) float small_lds[];  // SS::floats(layers, stage_small) floats
     FwdRegs<M, CS::W> R;
     std::conditional_t<CollectFwd<M, O, BF16>::SPLIT, SkStream<8 / CS::W>, char> wst;  // split forward's weights
 
@@ -159,15 +188,17 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     // small parameters) measured slower at 4096 and 262144 envs, fp32 and bf16
     if (stage_small) {  // ordered before the forwards by the barrier below
         const int lnf = (int)(a.policy.layers + 1) * 2 * kEmbed;
+        const bool all = stage_small == SS::kAll;
         float* win = small_lds;
-        float* bin = win + SS::WIN;
+        float* bin = win + (all ? SS::WIN : 0);
         float* ln = bin + SS::BIN;
         float* wh = ln + lnf;
-        for (int k = tid; k < SS::WIN; k += CS::NT) win[k] = sp.win[k];
+        if (all)
+            for (int k = tid; k < SS::WIN; k += CS::NT) win[k] = sp.win[k];
         for (int k = tid; k < SS::BIN; k += CS::NT) bin[k] = sp.bin[k];
         for (int k = tid; k < lnf; k += CS::NT) ln[k] = sp.ln[k];
         for (int k = tid; k < SS::WH; k += CS::NT) wh[k] = sp.wh[k];
-        sp = {win, bin, ln, wh};
+        sp = {all ? win : sp.win, bin, ln, wh};
     }
 
     if (envLane) {
@@ -190,22 +221,22 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
             store_floats<O>(a.obs_slots + (size_t)i * O, obs);
         }
 #pragma unroll
-        for (int k = 0; k < O; ++k) sm.obs[tid * O + k] = obs[k];
+        for (int k = 0; k < O; ++k) sm.obs()[tid * O + k] = obs[k];
     }
     __syncthreads();
 
     for (uint32_t t = 0; t <= T; ++t) {
         if constexpr (CollectFwd<M, O, BF16>::SPLIT)
-            split_forward16<CS::W, O>(a.policy, sp, sm.fwd, wst, t == 0, sm.obs, sm.head, HD);
+            split_forward16<CS::W, O>(a.policy, sp, sm.fwd, wst, t == 0, sm.obs(), sm.head(), HD);
         else if constexpr (BF16)
-            policy_forward_b<M, CS::W, HD, OE>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward_b<M, CS::W, HD, OE>(a.policy, sp, sm.fwd, R, sm.obs(), O, sm.head(), HD);
         else
             // global weight loads when the env states sit in LDS: there the
             // buffer loads' scalar descriptors cost the heightmap env more
             // spilling than they save (VoxelNav at 262144 envs, 135 -> 151 ms)
-            policy_forward<M, CS::W, !LS::USE, HD, OE>(a.policy, sp, sm.fwd, R, sm.obs, O, sm.head, HD);
+            policy_forward<M, CS::W, !LS::USE, HD, OE>(a.policy, sp, sm.fwd, R, sm.obs(), O, sm.head(), HD);
         if (envLane) {
-            const float* h = sm.head + tid * HD;
+            const float* h = sm.head() + tid * HD;
             if (t == T) {  // bootstrap head for GAE and headValue()
 #pragma unroll
                 for (int j = 0; j < HD; ++j) a.head_out[(size_t)i * HD + j] = h[j];
@@ -230,7 +261,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
 #pragma unroll
                     for (int q = KS; q < O; ++q) {
                         a.obs_slots[(k + n) * O + q] = of[q];
-                        sm.obs[tid * O + q] = of[q];
+                        sm.obs()[tid * O + q] = of[q];
                     }
                 } else {
                     Env::step(S(), act, o, r, done);
@@ -238,7 +269,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
                     for (int q = 0; q < O; ++q) obs[q] = of[q];
                     store_floats<O>(a.obs_slots + (k + n) * O, obs);
 #pragma unroll
-                    for (int q = 0; q < O; ++q) sm.obs[tid * O + q] = obs[q];
+                    for (int q = 0; q < O; ++q) sm.obs()[tid * O + q] = obs[q];
                 }
                 a.reward_slots[k] = r;
                 a.done_slots[k] = done;
@@ -254,7 +285,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
                     const State& se = LS::USE ? *reinterpret_cast<const State*>(lds_state + e * LS::STRIDE)
                                               : states[(size_t)blockIdx.x * M + e];
                     const float v = Env::observePart(se, p);
-                    sm.obs[e * O + p] = v;
+                    sm.obs()[e * O + p] = v;
                     a.obs_slots[row0 + (size_t)e * O + p] = v;
                 }
             }
@@ -293,10 +324,13 @@ void launch_collect_mw(const mg_collect_args* a, hipStream_t st) {
     using SS = SmallStage<Env, M, BF16>;
     constexpr size_t kPerWg = (size_t)163840 / CollectShape<M, Env::OBS_DIM, WIDE>::MIN_WG;  // LDS per workgroup
     const size_t stat = collect_static_lds<Env, M, BF16, WIDE>();
-    const size_t dyn = (size_t)SS::floats(a->policy.layers) * 4;
-    const bool stage = stat <= kPerWg && dyn <= kPerWg - stat;
+    const size_t all = (size_t)SS::floats(a->policy.layers, SS::kAll) * 4;
+    const size_t nowin = (size_t)SS::floats(a->policy.layers, SS::kNoWin) * 4;
+    const size_t room = stat <= kPerWg ? kPerWg - stat : 0;
+    const uint32_t stage = all <= room ? SS::kAll : nowin <= room ? SS::kNoWin : SS::kNone;
+    const size_t dyn = stage == SS::kAll ? all : stage == SS::kNoWin ? nowin : 0;
     const dim3 grid(a->n / M), block(CollectShape<M, Env::OBS_DIM, WIDE>::NT);
-    hipLaunchKernelGGL((collect_kernel<Env, M, BF16, WIDE>), grid, block, stage ? dyn : 0, st, *a, stage ? 1u : 0u);
+    hipLaunchKernelGGL((collect_kernel<Env, M, BF16, WIDE>), grid, block, dyn, st, *a, stage);
 }
 
 // An env with a split observation runs WIDE where the grid has at least two
