@@ -147,6 +147,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     // so the other threads could not read it: such an env always calls step().
     constexpr uint32_t KS = LS::USE || (WIDE && !Tr::STATE_IN_REGISTERS) ? Tr::OBS_SPLIT : 0;
     __shared__ CollectSmem<M, O, HD, BF16> sm;
+    static_assert(sizeof(CollectSmem<M, O, HD, BF16>) % 16 == 0, "the staged small parameters start 16-byte aligned");
     __shared__ uint32_t lds_state[LS::USE ? M * LS::STRIDE : 1];
     using SS = SmallStage<Env, M, BF16>;
     extern __shared__ __align__(16) float small_lds[];  // SS::floats(layers, stage_small) floats
