@@ -36,7 +36,7 @@ struct alignas(16) SkSmem {
     float xn[(Sh::LAYERS + 1) * kTR * kEmbed];  // LN captures for the backward
     float rstd[(Sh::LAYERS + 1) * kTR];  // 1 / sigma of every LN
     float ln[(Sh::LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
-    float wh[kEmbed * Sh::HEAD];              // W_head
+    float wh[kEmbed * Sh::HEAD];              // W_head, row k at k HC (HC columns, zero past HD)
     float obs[kTR * Sh::OBS];
     float acts[kTR * Sh::HEAD];  // the tile's float actions (Gaussian head)
     float lstd[Sh::HEAD];        // log_std (Gaussian head)
@@ -124,20 +124,25 @@ __device__ __forceinline__ void sk_ln_sums(const SkSmem<W>& L, float* tp_gamma, 
 }
 
 // model/linear.metal:17-37 for one row held by TPR lanes: hv[j] = x_f[row] .
-// W_head[:, j] for j < HD (0 for HD <= j < HC), the HC column sums reduced
-// together, so every lane of the row holds the whole head. wh: W_head in LDS.
+// W_head[:, j] (0 for HD <= j < HC), the HC column sums reduced together, so
+// every lane of the row holds the whole head. wh: W_head in LDS with rows of
+// HC columns, zero past HD, read as float4s (3 or 7 scalar reads per row with
+// HD columns).
 template <int TPR, int HC, int NV>
-__device__ __forceinline__ void sk_head(const RowVec<NV>& x, const float* wh, int HD, int c0, float (&hv)[HC]) {
+__device__ __forceinline__ void sk_head(const RowVec<NV>& x, const float* wh, int c0, float (&hv)[HC]) {
+    static_assert(HC % 4 == 0, "float4 rows");
     constexpr int CPT = 4 * NV;
 #pragma unroll
-    for (int j = 0; j < HC; ++j) {
-        float acc = 0.0f;
+    for (int j = 0; j < HC; ++j) hv[j] = 0.0f;
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const float w = wh[(c0 + c) * HD + j];  // in the LDS array for every j < HC
-            acc += x[c] * (j < HD ? w : 0.0f);
+    for (int c = 0; c < CPT; ++c) {
+        const float* wr = wh + (c0 + c) * HC;
+#pragma unroll
+        for (int q = 0; q < HC / 4; ++q) {
+            const f32x4 w = *reinterpret_cast<const f32x4*>(wr + 4 * q);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hv[4 * q + i] += x[c] * w[i];
         }
-        hv[j] = acc;
     }
     group_sum_n<TPR, HC>(hv);
 }
@@ -254,7 +259,7 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     float* const winL = &L.red[0][0];  // the partial buffer is unused until the first block's reduction
     float* const binL = winL + Sh::OBS * kEmbed;
     const float* lnp = pv.params + pv.off_ln_gamma[0];
-    const int n_obs = M * O, n_wh = kEmbed * HD, n_win = O * kEmbed, n_ln = (NL + 1) * 2 * kEmbed;
+    const int n_obs = M * O, n_win = O * kEmbed, n_ln = (NL + 1) * 2 * kEmbed;
     {
         // W_in as float4s, all of a thread's issued with the other first loads
         // (VoxelNav16's 3840 floats four loads at a time took two memory round
@@ -262,7 +267,14 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         constexpr int NW4 = (Sh::OBS * kEmbed / 4 + NT - 1) / NT;
         const int n_win4 = n_win / 4;  // O x 128 floats
         const float o0 = tid < n_obs ? a.obs_slots[g0 * O + tid] : 0.0f;
-        const float h0 = tid < n_wh ? pv.params[pv.off_head + tid] : 0.0f;
+        // W_head in rows of HC columns, zero past HD
+        constexpr int NWH = (kEmbed * HC + NT - 1) / NT;
+        float hw[NWH];
+#pragma unroll
+        for (int u = 0; u < NWH; ++u) {
+            const int idx = tid + u * NT, k = idx / HC, j = idx % HC;
+            hw[u] = idx < kEmbed * HC && j < HD ? pv.params[pv.off_head + k * HD + j] : 0.0f;
+        }
         f32x4 wv[NW4];
 #pragma unroll
         for (int u = 0; u < NW4; ++u) {
@@ -274,7 +286,9 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         const float l0 = tid < n_ln ? lnp[tid] : 0.0f;
         const float l1 = tid + NT < n_ln ? lnp[tid + NT] : 0.0f;
         if (tid < n_obs) L.obs[tid] = o0;
-        if (tid < n_wh) L.wh[tid] = h0;
+#pragma unroll
+        for (int u = 0; u < NWH; ++u)
+            if (tid + u * NT < kEmbed * HC) L.wh[tid + u * NT] = hw[u];
 #pragma unroll
         for (int u = 0; u < NW4; ++u)
             if (tid + u * NT < n_win4) *reinterpret_cast<f32x4*>(winL + 4 * (tid + u * NT)) = wv[u];
@@ -286,8 +300,6 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     // need no second element)
 #pragma unroll 4
     for (int idx = tid + NT; idx < n_obs; idx += NT) L.obs[idx] = a.obs_slots[g0 * O + idx];
-#pragma unroll 4
-    for (int idx = tid + NT; idx < n_wh; idx += NT) L.wh[idx] = pv.params[pv.off_head + idx];
 #pragma unroll 4
     for (int idx = tid + 2 * NT; idx < n_ln; idx += NT) L.ln[idx] = lnp[idx];
     const int A = (int)pv.act_dim;
@@ -366,7 +378,7 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         if (lk == 0) L.rstd[NL * M + row] = sd;
         rv_store(L.xs + row * kLds + c0, x);  // x_f for dW_head
         float hv[HC], dz[HC], dls[HC], st[5];
-        sk_head<TPR, HC>(x, L.wh, HD, c0, hv);
+        sk_head<TPR, HC>(x, L.wh, c0, hv);
         sk_loss_row<HC>(a, hv, A, pv.continuous != 0, L.lstd, L.acts + row * A, an, oldLp, ret, act, dz, dls, st);
         // lane lk < HD of the row writes head column lk and its gradient
         float hm = 0.0f, dm = 0.0f, lm = 0.0f;
@@ -388,12 +400,15 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         // model/linear.metal:40-60: the gradient at the final LN output, then its LN
         RowVec<NV> g = rv_zero<NV>();
 #pragma unroll
-        for (int j = 0; j < HC; ++j)
+        for (int c = 0; c < CPT; ++c) {
+            const float* wr = L.wh + (c0 + c) * HC;
 #pragma unroll
-            for (int c = 0; c < CPT; ++c) {
-                const float w = L.wh[(c0 + c) * HD + j];
-                g[c] += dz[j] * (j < HD ? w : 0.0f);
+            for (int q = 0; q < HC / 4; ++q) {
+                const f32x4 w = *reinterpret_cast<const f32x4*>(wr + 4 * q);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) g[c] += dz[4 * q + i] * w[i];
             }
+        }
         D = sk_layernorm_bwd<W>(L, g, NL, row, c0);
     }
     __syncthreads();  // dhead, dls, the LossStats terms and the LN's part terms written
