@@ -58,20 +58,31 @@ __device__ __forceinline__ float dpp_lane(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
-// v of lane L (a scalar read; every lane of the wave must be active).
-template <int L>
-__device__ __forceinline__ float lane_value(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), L));
+// The values of lane l and lane l ^ 16 (X = 16: v_permlane16_swap, which
+// exchanges the odd rows of its first operand with the even rows of its
+// second, 16 lanes a row) or lane l ^ 32 (X = 32: v_permlane32_swap, the
+// upper half of the first with the lower half of the second), both operands
+// copies of v: the first then holds the lower lane's value and the second the
+// upper lane's. Written as inline assembly because the compiler folds the
+// builtins' two results into one when both inputs are the same value; the
+// s_nop gives the two wait states a swap needs after a VALU write of its
+// operands (the copies). Every lane of the wave must be active.
+template <int X>
+__device__ __forceinline__ void lane_pair(float v, float& lower, float& upper) {
+    static_assert(X == 16 || X == 32, "row or half-wave partner");
+    lower = v, upper = v;
+    if constexpr (X == 16)
+        asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(lower), "+v"(upper));
+    else
+        asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lower), "+v"(upper));
 }
 
 // Sum over groups of G consecutive lanes (G a power of two <= 64); every lane
 // of a group gets the same bits. Inside a 16-lane row the partners come from
 // DPP moves (quad_perm xor 1, xor 2, then the half-row and row mirrors, each
-// pairing the group's halves). Across rows the four row sums are read as
-// scalars (v_readlane, no LDS round trip) and added pairwise: rows 0 + 1 and
-// 2 + 3 for G = 32, then those two for G = 64 (the same sums, in the same
-// order up to commutation, as shuffling lanes l ^ 16 and l ^ 32). Every lane
-// of the wave must be active.
+// pairing the group's halves); across rows from the permlane swaps (lane
+// l ^ 16, then l ^ 32), each pair added lower lane first. Every lane of the
+// wave must be active.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
     static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "power-of-two group");
@@ -80,11 +91,14 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 8) v += dpp_lane<0x141>(v);  // row_half_mirror
     if constexpr (G >= 16) v += dpp_lane<0x140>(v); // row_mirror
     if constexpr (G >= 32) {
-        const float lo = lane_value<0>(v) + lane_value<16>(v), hi = lane_value<32>(v) + lane_value<48>(v);
-        if constexpr (G == 32)
-            v = (threadIdx.x & 32) ? hi : lo;
-        else
-            v = lo + hi;
+        float lo, hi;
+        lane_pair<16>(v, lo, hi);
+        v = lo + hi;
+    }
+    if constexpr (G >= 64) {
+        float lo, hi;
+        lane_pair<32>(v, lo, hi);
+        v = lo + hi;
     }
     return v;
 }
@@ -106,16 +120,20 @@ __device__ __forceinline__ void group_sum_n(float (&v)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
         if constexpr (G >= 16) v[i] += dpp_lane<0x140>(v[i]);
-    if constexpr (G >= 32) {
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const float lo = lane_value<0>(v[i]) + lane_value<16>(v[i]), hi = lane_value<32>(v[i]) + lane_value<48>(v[i]);
-            if constexpr (G == 32)
-                v[i] = (threadIdx.x & 32) ? hi : lo;
-            else
-                v[i] = lo + hi;
+    for (int i = 0; i < N; ++i)
+        if constexpr (G >= 32) {
+            float lo, hi;
+            lane_pair<16>(v[i], lo, hi);
+            v[i] = lo + hi;
         }
-    }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if constexpr (G >= 64) {
+            float lo, hi;
+            lane_pair<32>(v[i], lo, hi);
+            v[i] = lo + hi;
+        }
 }
 
 // Sum of t[0..N) as a pairwise tree (t[c] + t[c + N/2], then halves again),
@@ -139,12 +157,14 @@ __device__ __forceinline__ float group_max(float v) {
     if constexpr (G >= 8) v = fmaxf(v, dpp_lane<0x141>(v));
     if constexpr (G >= 16) v = fmaxf(v, dpp_lane<0x140>(v));
     if constexpr (G >= 32) {
-        const float lo = fmaxf(lane_value<0>(v), lane_value<16>(v));
-        const float hi = fmaxf(lane_value<32>(v), lane_value<48>(v));
-        if constexpr (G == 32)
-            v = (threadIdx.x & 32) ? hi : lo;
-        else
-            v = fmaxf(lo, hi);
+        float lo, hi;
+        lane_pair<16>(v, lo, hi);
+        v = fmaxf(lo, hi);
+    }
+    if constexpr (G >= 64) {
+        float lo, hi;
+        lane_pair<32>(v, lo, hi);
+        v = fmaxf(lo, hi);
     }
     return v;
 }
