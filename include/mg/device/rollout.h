@@ -133,20 +133,38 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
     for (uint32_t k = tid; k < ne * SD; k += 256) gst[k] = lds[(k / SD) * STRIDE + k % SD];
 }
 
-// rollout_split_kernel with E envs per workgroup; E grows with n so the grid
-// stays at 1 K to 16 K workgroups (VoxelNav, random actions, 32 steps, in M env
-// steps/s against one lane per env: 183 / 16.3 at 4096 envs with E = 4, 414 /
-// 65 at 16384 with E = 8, 691 / 196 at 65536 and 853 / 437 at 262144 with E =
-// 16).
+template <typename Env, int MODE, int E>
+void launch_split_e(const mg_rollout_args* a, hipStream_t st) {
+    hipLaunchKernelGGL((rollout_split_kernel<Env, MODE, E>), dim3((a->n + E - 1) / E), dim3(256), 0, st, *a);
+}
+
+// rollout_split_kernel with E envs per workgroup: at most as many as keep the
+// workgroup's staged states within 17 KB of LDS, so that eight workgroups
+// (the 32 waves a CU holds) fit a CU's 160 KB, and fewer at small n, so the
+// grid stays at 1 K to 16 K workgroups. Each step is a short chain of
+// dependent LDS accesses and two barriers, so the more workgroups a CU
+// interleaves the better: VoxelNav16 (4 KB states), random actions, 262144
+// envs: 2.56 ms per 32-step launch with 16 envs per workgroup (two per CU),
+// 1.79 with 8, 1.49 with 4 (eight per CU); 4 envs on 128 or 64 threads 1.65
+// and 2.30, one env per wave 2.0. The heightmap VoxelNav (1 KB states, 16 per
+// workgroup, in M env steps/s against one lane per env: 183 / 16.3 at 4096
+// envs with E = 4, 414 / 65 at 16384 with E = 8, 691 / 196 at 65536 and
+// 853 / 437 at 262144 with E = 16).
 template <typename Env, int MODE>
 void launch_split_rollout(const mg_rollout_args* a, hipStream_t st) {
+    constexpr uint32_t fit = 17408u / (SplitRollout<Env>::STRIDE * 4u);  // states in 17 KB
+    constexpr int EL = fit >= 16 ? 16 : fit >= 8 ? 8 : fit >= 4 ? 4 : fit >= 2 ? 2 : 1;
     const uint32_t n = a->n;
-    if (n <= 4096u)
-        hipLaunchKernelGGL((rollout_split_kernel<Env, MODE, 4>), dim3((n + 3) / 4), dim3(256), 0, st, *a);
-    else if (n <= 32768u)
-        hipLaunchKernelGGL((rollout_split_kernel<Env, MODE, 8>), dim3((n + 7) / 8), dim3(256), 0, st, *a);
+    const int en = n <= 4096u ? 4 : (n <= 32768u ? 8 : 16);
+    const int e = EL < en ? EL : en;  // 16, 8, 4, or EL below 4
+    if constexpr (EL >= 16)
+        if (e == 16) return launch_split_e<Env, MODE, 16>(a, st);
+    if constexpr (EL >= 8)
+        if (e == 8) return launch_split_e<Env, MODE, 8>(a, st);
+    if constexpr (EL >= 4)
+        launch_split_e<Env, MODE, 4>(a, st);
     else
-        hipLaunchKernelGGL((rollout_split_kernel<Env, MODE, 16>), dim3((n + 15) / 16), dim3(256), 0, st, *a);
+        launch_split_e<Env, MODE, EL>(a, st);
 }
 
 // Returns 0, a positive hipError_t on a launch failure, or MG_ERR_INVALID.

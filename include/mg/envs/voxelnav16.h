@@ -68,16 +68,15 @@ struct VoxelNav16 {
 
     MG_HD static void reset(State& s, uint32_t& rng) {
         for (int w = 0; w < CELLS / 16; ++w) {
-            uint32_t r = rngNext(rng);
+            const uint32_t r = rngNext(rng);
+            // bit 2 c of f is set iff the 2-bit field c of r is 3; cells 4 q ..
+            // 4 q + 3 are bits 8 q, 8 q + 2, 8 q + 4, 8 q + 6 of f, and the
+            // multiply by 2^0 + 2^6 + 2^12 + 2^18 moves bit 2 j of x to bit 8 j
+            // (the other products land on bits 2 i + 6 k, two at most on one
+            // bit, whose carries go to bits 7, 13 and 19, masked off)
+            const uint32_t f = r & (r >> 1) & 0x55555555u;
             uint32_t packed[4];
-            for (int q = 0; q < 4; ++q) {
-                uint32_t word = 0;
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t f = (r >> (2 * (4 * q + j))) & 3u;
-                    word |= (uint32_t)(f == 3u) << (8 * j);
-                }
-                packed[q] = word;
-            }
+            for (int q = 0; q < 4; ++q) packed[q] = (((f >> (8 * q)) & 0x55u) * 0x41041u) & 0x01010101u;
             __builtin_memcpy(s.grid + 16 * w, packed, 16);
         }
         int a = draw_free_cell(s, rng, -1);

@@ -42,14 +42,16 @@ def test_random_rollout_bit_exact(mg, orc, env, n, steps, seed):
 @pytest.mark.parametrize("env,n,steps,reps,seed", [
     ("voxelnav", 4100, 40, 7, 4),      # 8 envs per workgroup, the last workgroup partial
     ("voxelnav", 33000, 20, 13, 5),    # 16 envs per workgroup, the last workgroup partial
-    ("voxelnav16", 4100, 40, 7, 6),    # 4 KB states, 8 per workgroup (33 KB of LDS)
-    ("voxelnav16", 33000, 20, 13, 7),  # 16 per workgroup (66 KB of LDS)
+    ("voxelnav16", 4099, 40, 7, 6),    # 4 KB states: 4 per workgroup (16.5 KB of LDS), the last partial
+    ("voxelnav16", 33001, 20, 13, 7),  # 4 per workgroup at any n, the last partial
 ])
 def test_split_rollout_sizes_bit_exact(mg, orc, env, n, steps, reps, seed):
     """The split-observation rollouts (VoxelNav's ray casts, VoxelNav16's
     neighbourhood cells, spread over each workgroup) at the env counts that
-    give 8 and 16 envs per workgroup, run past the 250- and 256-step caps so
-    that every env resets at least once."""
+    give VoxelNav 8 and 16 envs per workgroup, run past the 250- and 256-step
+    caps so that every env resets at least once (VoxelNav16's split reset
+    fills a workgroup's flagged grids on all its threads, several envs in one
+    step at the first step and at the cap)."""
     eid, kernel = ENVS[env]
     gym = mg.Gym(kernel, n, seed)
     g = orc.GymState(eid, n, seed)
