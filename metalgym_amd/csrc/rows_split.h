@@ -247,54 +247,78 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     const int n16 = lane & 15, q4 = 4 * (lane >> 4);
     float* tp = ws.tp + (size_t)blockIdx.x * ws.tp_count;
 
-    // start-up: the weight stream's first loads, then every small array's
-    // first element per thread before any is stored, so the staging's one
-    // memory round trip overlaps the weights' instead of preceding it
+    // start-up: every small array's first element per thread is loaded
+    // first (branch-free: out-of-range threads load an element in range and
+    // drop it), then the weight stream's first loads; the staging stores
+    // then wait for the small loads alone (vector memory loads complete in
+    // order), so the embed and LN0 overlap the arrival of the first weights
     const int rot = (wave + (int)(blockIdx.x >> 3)) % NC;
     const SkSeq<S> seq{pv.frag_fwd16 + pv.float_group, pv.frag_bwd16 + pv.float_group, NL, NC, wave, rot,
                        (uint32_t)kEmbed * (uint32_t)H};
     SkPos pos{0, 0, 0};
     SkStream<S> wst;
-    wst.start(seq, pos);
     float* const winL = &L.red[0][0];  // the partial buffer is unused until the first block's reduction
     float* const binL = winL + Sh::OBS * kEmbed;
     const float* lnp = pv.params + pv.off_ln_gamma[0];
     const int n_obs = M * O, n_win = O * kEmbed, n_ln = (NL + 1) * 2 * kEmbed;
+    const int A = (int)pv.act_dim;
+    float an, oldLp, ret;
+    int act = 0;
     {
         // W_in as float4s, all of a thread's issued with the other first loads
         // (VoxelNav16's 3840 floats four loads at a time took two memory round
         // trips of the start-up)
         constexpr int NW4 = (Sh::OBS * kEmbed / 4 + NT - 1) / NT;
         const int n_win4 = n_win / 4;  // O x 128 floats
-        const float o0 = tid < n_obs ? a.obs_slots[g0 * O + tid] : 0.0f;
+        float o0 = a.obs_slots[g0 * O + (tid < n_obs ? tid : n_obs - 1)];
         // W_head in rows of HC columns, zero past HD
         constexpr int NWH = (kEmbed * HC + NT - 1) / NT;
         float hw[NWH];
 #pragma unroll
         for (int u = 0; u < NWH; ++u) {
             const int idx = tid + u * NT, k = idx / HC, j = idx % HC;
-            hw[u] = idx < kEmbed * HC && j < HD ? pv.params[pv.off_head + k * HD + j] : 0.0f;
+            const bool in = idx < kEmbed * HC && j < HD;
+            hw[u] = pv.params[pv.off_head + (in ? k * HD + j : 0)];
         }
         f32x4 wv[NW4];
 #pragma unroll
         for (int u = 0; u < NW4; ++u) {
             const int i4 = tid + u * NT;
-            wv[u] = i4 < n_win4 ? *reinterpret_cast<const f32x4*>(pv.params + pv.off_in_w + 4 * i4)
-                                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            wv[u] = *reinterpret_cast<const f32x4*>(pv.params + pv.off_in_w + 4 * (i4 < n_win4 ? i4 : n_win4 - 1));
         }
-        const float b0 = tid < kEmbed ? pv.params[pv.off_in_b + tid] : 0.0f;
-        const float l0 = tid < n_ln ? lnp[tid] : 0.0f;
-        const float l1 = tid + NT < n_ln ? lnp[tid + NT] : 0.0f;
+        const float b0 = pv.params[pv.off_in_b + (tid < kEmbed ? tid : 0)];
+        const float l0 = lnp[tid < n_ln ? tid : 0];
+        const float l1 = lnp[tid + NT < n_ln ? tid + NT : 0];
+        float av = 0.0f, ls = 0.0f;
+        if (pv.continuous) {  // the Gaussian head's inputs of the loss
+            av = static_cast<const float*>(a.action_slots)[g0 * A + (tid < M * A ? tid : 0)];
+            ls = pv.params[pv.off_log_std + (tid < A ? tid : 0)];
+        }
+        {
+            const size_t gr = g0 + row;
+            const float mean = a.adv_stats[2 * a.step.block], inv = a.adv_stats[2 * a.step.block + 1];
+            an = (a.adv_slots[gr] - mean) * inv;
+            oldLp = a.logp_slots[gr];
+            ret = a.ret_slots[gr];
+            if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
+        }
+        wst.start(seq, pos);
         if (tid < n_obs) L.obs[tid] = o0;
 #pragma unroll
-        for (int u = 0; u < NWH; ++u)
-            if (tid + u * NT < kEmbed * HC) L.wh[tid + u * NT] = hw[u];
+        for (int u = 0; u < NWH; ++u) {
+            const int idx = tid + u * NT;
+            if (idx < kEmbed * HC) L.wh[idx] = idx % HC < HD ? hw[u] : 0.0f;
+        }
 #pragma unroll
         for (int u = 0; u < NW4; ++u)
             if (tid + u * NT < n_win4) *reinterpret_cast<f32x4*>(winL + 4 * (tid + u * NT)) = wv[u];
         if (tid < kEmbed) binL[tid] = b0;
         if (tid < n_ln) L.ln[tid] = l0;
         if (tid + NT < n_ln) L.ln[tid + NT] = l1;
+        if (pv.continuous) {
+            if (tid < M * A) L.acts[tid] = av;
+            if (tid < A) L.lstd[tid] = ls;
+        }
     }
     // the rest, four elements' loads ahead of their stores (CartPole's arrays
     // need no second element)
@@ -302,22 +326,6 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     for (int idx = tid + NT; idx < n_obs; idx += NT) L.obs[idx] = a.obs_slots[g0 * O + idx];
 #pragma unroll 4
     for (int idx = tid + 2 * NT; idx < n_ln; idx += NT) L.ln[idx] = lnp[idx];
-    const int A = (int)pv.act_dim;
-    if (pv.continuous) {  // the Gaussian head's inputs of the loss
-        const float* af = static_cast<const float*>(a.action_slots) + g0 * A;
-        if (tid < M * A) L.acts[tid] = af[tid];
-        if (tid < A) L.lstd[tid] = pv.params[pv.off_log_std + tid];
-    }
-    float an, oldLp, ret;
-    int act = 0;
-    {
-        const size_t gr = g0 + row;
-        const float mean = a.adv_stats[2 * a.step.block], inv = a.adv_stats[2 * a.step.block + 1];
-        an = (a.adv_slots[gr] - mean) * inv;
-        oldLp = a.logp_slots[gr];
-        ret = a.ret_slots[gr];
-        if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
-    }
     __syncthreads();
 
     float* const cx = ws.x;
