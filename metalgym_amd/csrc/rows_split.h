@@ -478,8 +478,10 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     // model/input.metal:38-60 on this tile: dW_in[k][c] = sum_r obs[r][k] dh0[r][c], db_in = sum_r dh0
     rv_store(L.xs + row * kLds + c0, D);
     __syncthreads();
+    // LN0's sums on threads 0 .. 255 and db_in's on the waves past them (on 8
+    // waves: 256 .. 383), so no wave adds two of the tail's column sums
     sk_ln_sums<W>(L, tp + pv.off_ln_gamma[0], tp + pv.off_ln_beta[0]);
-    tile_colsum2<M>(L.xs, nullptr, tp + pv.off_in_b, nullptr);
+    tile_colsum2<M>(L.xs, nullptr, tp + pv.off_in_b, nullptr, NT >= 3 * kEmbed ? 2 * kEmbed : 0);
     tile_outer<M, NT>(L.obs, O, O, L.xs, tp + pv.off_in_w, kEmbed, 1);
 }
 

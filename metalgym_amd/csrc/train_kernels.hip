@@ -100,11 +100,12 @@ __device__ __forceinline__ void tile_outer(const float* a, int lda, int K, const
 
 // Column sums of an LDS tile of M rows (sum_r b[r * kLds + c]) and, if a is
 // given, of its products with another tile (sum_r a[r * kEmbed + c] b[...]),
-// rows in order; threads 0..127 one column each. No barrier.
+// rows in order; threads t0 .. t0 + 127 one column each. No barrier.
 template <int M>
-__device__ __forceinline__ void tile_colsum2(const float* b, const float* a, float* out_sum, float* out_prod) {
-    const int c = threadIdx.x;
-    if (c < kEmbed) {
+__device__ __forceinline__ void tile_colsum2(const float* b, const float* a, float* out_sum, float* out_prod,
+                                             int t0 = 0) {
+    const int c = (int)threadIdx.x - t0;
+    if (c >= 0 && c < kEmbed) {
         float s = 0.0f, p = 0.0f;
 #pragma unroll
         for (int r = 0; r < M; ++r) {
