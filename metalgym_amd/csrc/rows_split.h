@@ -422,15 +422,18 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     __syncthreads();  // dhead, dls, the LossStats terms and the LN's part terms written
 
     // model/linear.metal:71-93 on this tile: dW_head[k][j] = sum_r x_f[r][k] dhead[r][j]
+    // (its outputs start at thread 0; the log_std and LossStats sums go to the
+    // last waves, which have the fewest of them)
     tile_outer<M, NT>(L.dhead, HD, HD, L.xs, tp + pv.float_group, 1, HD);
-    if (pv.continuous && tid < kEmbed) {  // model/gaussian.metal:166-168, summed over the tile in row order
+    const int tl = tid - (NT - kEmbed);  // thread index within the last 128
+    if (pv.continuous && tl >= 0) {  // model/gaussian.metal:166-168, summed over the tile in row order
         float s = 0.0f;
-        if (tid < A)
-            for (int r = 0; r < M; ++r) s += L.dls[r * A + tid];
-        tp[pv.off_log_std + tid] = s;  // and 0 in the arena padding after log_std (A <= 63 < 128)
+        if (tl < A)
+            for (int r = 0; r < M; ++r) s += L.dls[r * A + tl];
+        tp[pv.off_log_std + tl] = s;  // and 0 in the arena padding after log_std (A <= 63 < 128)
     }
-    if (tid >= 64 && tid < 64 + 5) {  // the tile's LossStats sums, in row order
-        const int qq = tid - 64;
+    if (tl >= 64 && tl < 64 + 5) {  // the tile's LossStats sums, in row order
+        const int qq = tl - 64;
         float s = 0.0f;
         for (int r = 0; r < M; ++r) s += L.stat[r * 5 + qq];
         tp[pv.float_group + kEmbed * HD + qq] = s;
