@@ -36,7 +36,7 @@ struct alignas(16) SkSmem {
     float xn[(Sh::LAYERS + 1) * kTR * kEmbed];  // LN captures for the backward
     float rstd[(Sh::LAYERS + 1) * kTR];  // 1 / sigma of every LN
     float ln[(Sh::LAYERS + 1) * 2 * kEmbed];  // gamma, beta of every LN
-    float wh[kEmbed * Sh::HEAD];              // W_head, row k at k HC (HC columns, zero past HD)
+    float wh[kEmbed * Sh::HEAD];              // W_head, HC columns (zero past HD), at sk_wh_index
     float obs[kTR * Sh::OBS];
     float acts[kTR * Sh::HEAD];  // the tile's float actions (Gaussian head)
     float lstd[Sh::HEAD];        // log_std (Gaussian head)
@@ -123,11 +123,22 @@ __device__ __forceinline__ void sk_ln_sums(const SkSmem<W>& L, float* tp_gamma, 
     }
 }
 
+// W_head (element (k, j): embed row k, head column j < HC) in LDS, laid out
+// for the row layout's reads: thread t of a row's TPR holds embed rows
+// k = CPT t + c and reads float4 q (columns 4 q .. 4 q + 3) of each, and run
+// (c, q) of the TPR threads is contiguous, 16 bytes a thread, so one float4
+// read of a wave touches consecutive banks. (Rows of HC floats in k order put
+// consecutive threads 4 HC floats apart, several of them on one bank for every
+// read: the head took 0.8 K cycles for CartPole and 2.7 K for VoxelNav16.)
+template <int TPR, int CPT, int HC>
+__device__ __forceinline__ int sk_wh_index(int k, int j) {
+    return (((k % CPT) * (HC / 4) + j / 4) * TPR + k / CPT) * 4 + j % 4;
+}
+
 // model/linear.metal:17-37 for one row held by TPR lanes: hv[j] = x_f[row] .
 // W_head[:, j] (0 for HD <= j < HC), the HC column sums reduced together, so
-// every lane of the row holds the whole head. wh: W_head in LDS with rows of
-// HC columns, zero past HD, read as float4s (3 or 7 scalar reads per row with
-// HD columns).
+// every lane of the row holds the whole head. wh: W_head in LDS at
+// sk_wh_index, zero past HD, read as float4s.
 template <int TPR, int HC, int NV>
 __device__ __forceinline__ void sk_head(const RowVec<NV>& x, const float* wh, int c0, float (&hv)[HC]) {
     static_assert(HC % 4 == 0, "float4 rows");
@@ -136,10 +147,9 @@ __device__ __forceinline__ void sk_head(const RowVec<NV>& x, const float* wh, in
     for (int j = 0; j < HC; ++j) hv[j] = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        const float* wr = wh + (c0 + c) * HC;
 #pragma unroll
         for (int q = 0; q < HC / 4; ++q) {
-            const f32x4 w = *reinterpret_cast<const f32x4*>(wr + 4 * q);
+            const f32x4 w = *reinterpret_cast<const f32x4*>(wh + sk_wh_index<TPR, CPT, HC>(c0 + c, 4 * q));
 #pragma unroll
             for (int i = 0; i < 4; ++i) hv[4 * q + i] += x[c] * w[i];
         }
@@ -271,7 +281,7 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         constexpr int NW4 = (Sh::OBS * kEmbed / 4 + NT - 1) / NT;
         const int n_win4 = n_win / 4;  // O x 128 floats
         float o0 = a.obs_slots[g0 * O + (tid < n_obs ? tid : n_obs - 1)];
-        // W_head in rows of HC columns, zero past HD
+        // W_head, HC columns a row, zero past HD
         constexpr int NWH = (kEmbed * HC + NT - 1) / NT;
         float hw[NWH];
 #pragma unroll
@@ -307,7 +317,7 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
 #pragma unroll
         for (int u = 0; u < NWH; ++u) {
             const int idx = tid + u * NT;
-            if (idx < kEmbed * HC) L.wh[idx] = idx % HC < HD ? hw[u] : 0.0f;
+            if (idx < kEmbed * HC) L.wh[sk_wh_index<TPR, CPT, HC>(idx / HC, idx % HC)] = idx % HC < HD ? hw[u] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < NW4; ++u)
@@ -337,6 +347,7 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
     RowVec<NV> h;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) h[c] = binL[c0 + c];
+#pragma unroll 4  // the LDS reads of four observations issued together
     for (int k = 0; k < O; ++k) {
         const float ok = L.obs[row * O + k];
 #pragma unroll
@@ -409,10 +420,9 @@ __global__ void __launch_bounds__(64 * W) train_rows_split_kernel(const RowsArgs
         RowVec<NV> g = rv_zero<NV>();
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
-            const float* wr = L.wh + (c0 + c) * HC;
 #pragma unroll
             for (int q = 0; q < HC / 4; ++q) {
-                const f32x4 w = *reinterpret_cast<const f32x4*>(wr + 4 * q);
+                const f32x4 w = *reinterpret_cast<const f32x4*>(L.wh + sk_wh_index<TPR, CPT, HC>(c0 + c, 4 * q));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) g[c] += dz[4 * q + i] * w[i];
             }
