@@ -179,7 +179,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
         // the tile's states are contiguous in device memory: dword k of the run
         // is dword k % SD of env k / SD
         const uint32_t* gin = reinterpret_cast<const uint32_t*>(states + (size_t)blockIdx.x * M);
-        for (uint32_t k = tid; k < M * LS::SD; k += CS::NT) lds_state[(k / LS::SD) * LS::STRIDE + k % LS::SD] = gin[k];
+        states_to_lds<LS::SD, LS::STRIDE, M, CS::NT>(lds_state, gin, M);
         __syncthreads();
     }
     float obs[O];
@@ -300,7 +300,7 @@ __global__ void __launch_bounds__((CollectShape<M, Env::OBS_DIM, WIDE>::NT),
     }
     if constexpr (LS::USE) {  // every env lane's last step is before the loop's final barrier
         uint32_t* gout = reinterpret_cast<uint32_t*>(states + (size_t)blockIdx.x * M);
-        for (uint32_t k = tid; k < M * LS::SD; k += CS::NT) gout[k] = lds_state[(k / LS::SD) * LS::STRIDE + k % LS::SD];
+        states_from_lds<LS::SD, LS::STRIDE, M, CS::NT>(lds_state, gout, M);
     }
 }
 

@@ -205,7 +205,67 @@ __device__ __forceinline__ void load_floats(float* dst, const float* src) {
     }
 }
 
-// A uniformly random action from the env's stream (D4 of the build plan):
+// The states of ne <= MAXE consecutive envs (SD dwords each, contiguous in
+// device memory at g) to LDS at STRIDE dwords per env, by NT threads, and back.
+// With SD a multiple of 4 and g 16-byte aligned: 16-byte accesses, and every
+// load of a thread issued before its first LDS store, so the workgroup waits
+// one memory round trip (a load-then-store loop waits one per iteration: 17
+// for four VoxelNav16 states).
+template <uint32_t SD, uint32_t STRIDE, uint32_t MAXE, int NT>
+__device__ __forceinline__ void states_to_lds(uint32_t* lds, const uint32_t* g, uint32_t ne) {
+    const uint32_t tid = threadIdx.x;
+    if constexpr (SD % 4 == 0) {
+        if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
+            constexpr uint32_t Q = SD / 4;
+            constexpr int NQ = (int)((MAXE * Q + NT - 1) / NT);
+            const uint32_t nq = ne * Q;  // ne >= 1
+            const uint4* g4 = reinterpret_cast<const uint4*>(g);
+            // Branch-free: a thread past the end loads and stores the last
+            // 16 bytes again (the same values to the same LDS dwords), so no
+            // load is sunk into a conditional store block behind the others.
+            uint32_t kk[NQ];
+            uint4 v[NQ];
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                const uint32_t k = tid + (uint32_t)(NT * u);
+                kk[u] = k < nq ? k : nq - 1;
+                v[u] = g4[kk[u]];
+            }
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                uint32_t* d = lds + (kk[u] / Q) * STRIDE + (kk[u] % Q) * 4;
+                d[0] = v[u].x, d[1] = v[u].y, d[2] = v[u].z, d[3] = v[u].w;
+            }
+            return;
+        }
+    }
+    for (uint32_t k = tid; k < ne * SD; k += NT) lds[(k / SD) * STRIDE + k % SD] = g[k];
+}
+
+template <uint32_t SD, uint32_t STRIDE, uint32_t MAXE, int NT>
+__device__ __forceinline__ void states_from_lds(const uint32_t* lds, uint32_t* g, uint32_t ne) {
+    const uint32_t tid = threadIdx.x;
+    if constexpr (SD % 4 == 0) {
+        if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
+            constexpr uint32_t Q = SD / 4;
+            constexpr int NQ = (int)((MAXE * Q + NT - 1) / NT);
+            const uint32_t nq = ne * Q;
+            uint4* g4 = reinterpret_cast<uint4*>(g);
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                const uint32_t k = tid + (uint32_t)(NT * u);
+                if (k < nq) {
+                    const uint32_t* s = lds + (k / Q) * STRIDE + (k % Q) * 4;
+                    g4[k] = make_uint4(s[0], s[1], s[2], s[3]);
+                }
+            }
+            return;
+        }
+    }
+    for (uint32_t k = tid; k < ne * SD; k += NT) g[k] = lds[(k / SD) * STRIDE + k % SD];
+}
+
+// A uniformly random action from the env's stream (this build's random policy):
 // rngInt(rng, ACT_DIM) for an integer action, uniform [-1, 1) per float.
 template <typename Env>
 __device__ __forceinline__ typename Env::Action random_action(uint32_t& rng) {

@@ -86,13 +86,12 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
     const uint32_t n = a.n, tid = threadIdx.x, e0 = blockIdx.x * E;
     const uint32_t ne = n - e0 < (uint32_t)E ? n - e0 : (uint32_t)E;  // envs of this workgroup
     uint32_t* gst = reinterpret_cast<uint32_t*>(static_cast<State*>(a.state) + e0);
-    for (uint32_t k = tid; k < ne * SD; k += 256) lds[(k / SD) * STRIDE + k % SD] = gst[k];
-    uint32_t rng = 0;
-    uint8_t done = 0;
-    if (tid < ne) {
-        rng = a.rng[e0 + tid];
-        done = a.done[e0 + tid];
-    }
+    // every thread loads an env's RNG and done flag (the env lanes keep theirs),
+    // branch-free and before the states, so all of it is one round trip
+    const uint32_t ei = e0 + (tid < ne ? tid : 0);
+    uint32_t rng = a.rng[ei];
+    uint8_t done = a.done[ei];
+    states_to_lds<SD, STRIDE, E, 256>(lds, gst, ne);
     __syncthreads();
     for (uint32_t t = 0; t < a.steps; ++t) {
         if (tid < ne) {
@@ -130,7 +129,7 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
         a.rng[e0 + tid] = rng;
         a.done[e0 + tid] = done;
     }
-    for (uint32_t k = tid; k < ne * SD; k += 256) gst[k] = lds[(k / SD) * STRIDE + k % SD];
+    states_from_lds<SD, STRIDE, E, 256>(lds, gst, ne);
 }
 
 template <typename Env, int MODE, int E>

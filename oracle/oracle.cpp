@@ -363,8 +363,9 @@ void env_step(int env, void* state, const void* action, float* obs, float& rewar
     }
 }
 
-// A random action drawn from the env's stream (D4): rngInt(rng, ACT_DIM) for a
-// discrete action, uniform [-1, 1) per dimension for a float action.
+// A random action drawn from the env's stream (this build's random policy):
+// rngInt(rng, ACT_DIM) for a discrete action, uniform [-1, 1) per dimension
+// for a float action.
 void random_action(int env, uint32_t& rng, void* out) {
     orc_env_info info = env_info(env);
     if (info.continuous) {
@@ -693,7 +694,8 @@ int orc_layout_get(const orc_dims* d, orc_layout* out) {
 
 uint64_t orc_splitmix_next(uint64_t* state) { return splitmix(*state); }
 
-// model/ppo.h:375-410 with D2: uniform init with the reference's per-layer std
+// model/ppo.h:375-410, drawn from SplitMix64 instead of the reference's
+// generator: uniform init with the reference's per-layer std
 // (bound = sqrt(3) std), drawn in the reference's parameter order.
 void orc_init_params(const orc_dims* dp, uint32_t seed, float* P) {
     const orc_dims& d = *dp;

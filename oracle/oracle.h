@@ -133,8 +133,9 @@ void orc_train_minibatch_masked(const orc_dims* d, const orc_hparams* hp, float*
                                 const float* ret, const float* old_logp, float* grad, orc_stats* stats,
                                 float* head_out, const uint8_t* relu_mask, float* preact_out, int threads);
 
-/* The build's minibatch order (D5): per epoch a Fisher-Yates shuffle of the
- * block ids driven by the model's shuffle stream. */
+/* This build's minibatch order (the reference has no random-access minibatch
+ * order of its own at n > 4096): per epoch a Fisher-Yates shuffle of the
+ * block ids driven by the model's SplitMix64 shuffle stream. */
 void orc_shuffle_state_init(uint32_t seed, uint64_t* state);
 void orc_shuffle_blocks(uint64_t* state, uint32_t* order, uint32_t count);
 

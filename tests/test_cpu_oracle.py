@@ -297,7 +297,7 @@ def test_gae_closed_form(orc):
     np.testing.assert_allclose(ret, want + value, rtol=1e-5, atol=1e-5)
 
 
-# ---- minibatch order (D5) ----------------------------------------------------------
+# ---- minibatch order (seeded block shuffle) ------------------------------------------
 
 def test_shuffle_is_a_seeded_permutation(orc):
     s, s2 = C.c_uint64(0), C.c_uint64(0)
