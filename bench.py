@@ -66,36 +66,70 @@ def bench_collect(kernel, n, T, steps, warmup, O, A, precision="fp32", layers=L)
     return gym, model, dt, times
 
 
-def rollout_bytes(gym, n, T):
+# Envs whose steps write only a leading header of State (STEP_WRITES in the
+# env's header, in bytes here): the split rollout writes the rest of an env's
+# state back only if the env reset during the launch.
+STEP_WRITE_BYTES = {"rollout_voxelnav16": 32}
+
+
+def rollout_bytes(gym, n, T, resets=None):
     """HBM bytes of one random rollout launch that no layout avoids: the T
-    slots (obs, action, reward, done) and each env's state, rng and done read
-    and written once. CartPole: 26.5 B per env-step. VoxelNav16: 129 B of
-    slots per env-step, its 4128-byte state once in and out per launch."""
+    slots (obs, action, reward, done), each env's rng and done read and written
+    once, and its state read once and written back once: whole, or for an env
+    of STEP_WRITE_BYTES its header plus, for each of the `resets` envs that
+    reset in the launch, the rest. CartPole: 26.5 B per env-step. VoxelNav16:
+    129 B of slots per env-step, its 4128-byte state read once per launch."""
     slot = 4 * gym.obs_dim + gym.action_bytes + 4 + 1
-    return n * T * slot + n * 2 * (gym.state_bytes + 4 + 1)
+    hdr = STEP_WRITE_BYTES.get(gym.kernel)
+    if hdr is None or resets is None:
+        return n * T * slot + n * 2 * (gym.state_bytes + 4 + 1)
+    return n * T * slot + n * 2 * (4 + 1) + n * (gym.state_bytes + hdr) + resets * (gym.state_bytes - hdr)
 
 
 def bench_random(n, T, reps, kernel="rollout_cartpole", hbm=True):
     """Random-policy rollouts, with the launch's unavoidable HBM bytes
     (rollout_bytes) over the kernel's event-timed duration."""
+    import numpy as np
     import metalgym_amd as mg
 
     gym = mg.Gym(kernel, n, 0)
     bufs = gym.rollout_random(T)
     sync()
+    # an env of STEP_WRITE_BYTES writes its whole state back only in a launch
+    # in which it resets, which it does iff its done flag was set at the end
+    # of the previous launch or at any step of this one but the last: each
+    # launch's done slots are read back after it (outside the timed sum)
+    partial = hbm and kernel in STEP_WRITE_BYTES
+    resets = 0
+    if partial:
+        dn = bufs[3]
+        prev = dn.download(np.uint8, (T, n))[T - 1].astype(bool)
     mg.timing_reset()
     mg.timing_enable(True)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        gym.rollout_random(T, bufs, sync=False)
-    sync()
-    dt = time.perf_counter() - t0
+    if partial:
+        dt = 0.0
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            gym.rollout_random(T, bufs, sync=False)
+            sync()
+            dt += time.perf_counter() - t0
+            d = dn.download(np.uint8, (T, n)).astype(bool)
+            resets += int((prev | d[:T - 1].any(axis=0)).sum())
+            prev = d[T - 1]
+    else:
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            gym.rollout_random(T, bufs, sync=False)
+        sync()
+        dt = time.perf_counter() - t0
     mg.timing_enable(False)
     times = mg.timing_get()
     kms = kernel_avg_ms(times, "rollout")
     out = {"env_steps_per_s": reps * n * T / dt, "kernel_us": kms * 1e3}
     if hbm:
-        bytes_launch = rollout_bytes(gym, n, T)
+        bytes_launch = rollout_bytes(gym, n, T, resets / reps if partial else None)
+        if partial:
+            out["resets_per_launch"] = resets / reps
         out["bytes_per_launch"] = bytes_launch
         out["hbm_GBps"] = bytes_launch / (kms * 1e-3) / 1e9
         out["hbm_frac"] = bytes_launch / (kms * 1e-3) / PEAK_HBM

@@ -242,19 +242,22 @@ __device__ __forceinline__ void states_to_lds(uint32_t* lds, const uint32_t* g, 
     for (uint32_t k = tid; k < ne * SD; k += NT) lds[(k / SD) * STRIDE + k % SD] = g[k];
 }
 
-template <uint32_t SD, uint32_t STRIDE, uint32_t MAXE, int NT>
-__device__ __forceinline__ void states_from_lds(const uint32_t* lds, uint32_t* g, uint32_t ne) {
+// Back to device memory: with HW < SD, of env e only dwords [0, HW) (rounded
+// up to 16 bytes on the vector path) unless full[e] (LDS) is non-zero.
+template <uint32_t SD, uint32_t STRIDE, uint32_t MAXE, int NT, uint32_t HW = SD>
+__device__ __forceinline__ void states_from_lds(const uint32_t* lds, uint32_t* g, uint32_t ne,
+                                                const uint32_t* full = nullptr) {
     const uint32_t tid = threadIdx.x;
     if constexpr (SD % 4 == 0) {
         if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
-            constexpr uint32_t Q = SD / 4;
+            constexpr uint32_t Q = SD / 4, HQ = (HW + 3) / 4;
             constexpr int NQ = (int)((MAXE * Q + NT - 1) / NT);
             const uint32_t nq = ne * Q;
             uint4* g4 = reinterpret_cast<uint4*>(g);
 #pragma unroll
             for (int u = 0; u < NQ; ++u) {
                 const uint32_t k = tid + (uint32_t)(NT * u);
-                if (k < nq) {
+                if (k < nq && (HQ >= Q || k % Q < HQ || full[k / Q])) {
                     const uint32_t* s = lds + (k / Q) * STRIDE + (k % Q) * 4;
                     g4[k] = make_uint4(s[0], s[1], s[2], s[3]);
                 }
@@ -262,7 +265,8 @@ __device__ __forceinline__ void states_from_lds(const uint32_t* lds, uint32_t* g
             return;
         }
     }
-    for (uint32_t k = tid; k < ne * SD; k += NT) g[k] = lds[(k / SD) * STRIDE + k % SD];
+    for (uint32_t k = tid; k < ne * SD; k += NT)
+        if (HW >= SD || k % SD < HW || full[k / SD]) g[k] = lds[(k / SD) * STRIDE + k % SD];
 }
 
 // A uniformly random action from the env's stream (this build's random policy):

@@ -82,7 +82,12 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
     using Obs = typename Env::Obs;
     constexpr int O = Env::OBS_DIM;
     constexpr uint32_t K = SR::K, SD = SR::SD, STRIDE = SR::STRIDE;
+    // an env whose steps write only its first HW dwords writes the rest back
+    // only if it reset during the launch (reset_in)
+    constexpr uint32_t HW = EnvTraits<Env>::STEP_WRITES;
+    constexpr bool PART = HW < SD;
     __shared__ uint32_t lds[E * STRIDE];
+    __shared__ uint32_t reset_in[PART ? E : 1];
     const uint32_t n = a.n, tid = threadIdx.x, e0 = blockIdx.x * E;
     const uint32_t ne = n - e0 < (uint32_t)E ? n - e0 : (uint32_t)E;  // envs of this workgroup
     uint32_t* gst = reinterpret_cast<uint32_t*>(static_cast<State*>(a.state) + e0);
@@ -92,6 +97,7 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
     uint32_t rng = a.rng[ei];
     uint8_t done = a.done[ei];
     states_to_lds<SD, STRIDE, E, 256>(lds, gst, ne);
+    if (PART && tid < (uint32_t)E) reset_in[tid] = 0;
     __syncthreads();
     for (uint32_t t = 0; t < a.steps; ++t) {
         if (tid < ne) {
@@ -104,7 +110,10 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
             } else {
                 act = static_cast<const Action*>(a.actions_in)[k];
             }
-            if (done) Env::reset(s, rng);
+            if (done) {
+                Env::reset(s, rng);
+                if constexpr (PART) reset_in[tid] = 1;
+            }
             Obs o{};
             float r = 0.0f;
             Env::stepState(s, act, r, done);
@@ -129,7 +138,7 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
         a.rng[e0 + tid] = rng;
         a.done[e0 + tid] = done;
     }
-    states_from_lds<SD, STRIDE, E, 256>(lds, gst, ne);
+    states_from_lds<SD, STRIDE, E, 256, HW>(lds, gst, ne, reset_in);  // reset_in: after the loop's last barrier
 }
 
 template <typename Env, int MODE, int E>

@@ -30,6 +30,14 @@
 // memory at two workgroups per CU) and, where the size is a multiple of 4, the
 // rollouts (the tile's states staged in LDS). The other shapes call step().
 //
+// Optional, for a large State whose steps change only its first fields:
+//
+//       static constexpr uint32_t STEP_WRITES = D;   // dwords
+//
+// promises that stepState (and step) write nothing past the first D dwords of
+// State; reset may write any. The rollouts that stage states in LDS then write
+// the rest of an env's state back only if the env reset during the launch.
+//
 // This mirrors the reference's Env template (README.md:21-66; rollout.h:31-54):
 // same member names, same reset/step contract, one struct instead of a Metal
 // twin plus a host twin. A .hip file that includes <mg/device/env_kernels.h> and
@@ -81,6 +89,15 @@ struct ObsSplit<Env, std::void_t<decltype(Env::OBS_SPLIT)>> {
     static constexpr uint32_t value = Env::OBS_SPLIT;
 };
 
+template <typename Env, typename = void>
+struct StepWrites {
+    static constexpr uint32_t value = (uint32_t)((sizeof(typename Env::State) + 3) / 4);
+};
+template <typename Env>
+struct StepWrites<Env, std::void_t<decltype(Env::STEP_WRITES)>> {
+    static constexpr uint32_t value = Env::STEP_WRITES;
+};
+
 template <typename Env>
 struct EnvTraits {
     using State = typename Env::State;
@@ -101,6 +118,9 @@ struct EnvTraits {
     // the optional split observation's part count (0: none)
     static constexpr uint32_t OBS_SPLIT = ObsSplit<Env>::value;
     static_assert(OBS_SPLIT <= OBS_DIM, "OBS_SPLIT counts floats of Obs");
+    // the leading dwords of State a step may write (all of them unless declared)
+    static constexpr uint32_t STEP_WRITES = StepWrites<Env>::value;
+    static_assert(STEP_WRITES >= 1 && STEP_WRITES <= (sizeof(State) + 3) / 4, "STEP_WRITES counts dwords of State");
 };
 
 }  // namespace mg

@@ -24,6 +24,8 @@
 // a split observation (OBS_SPLIT, env.h): independent gathers from the grid,
 // which the kernels spread over a workgroup's threads.
 #pragma once
+#include <stddef.h>
+
 #include "../env.h"
 
 struct VoxelNav16 {
@@ -91,6 +93,9 @@ struct VoxelNav16 {
     }
 
     static constexpr uint32_t OBS_SPLIT = 27;
+    // a step moves the agent and counts (px .. pad); the grid changes on reset only
+    static constexpr uint32_t STEP_WRITES = 8;
+    static_assert(offsetof(State, grid) == 4 * STEP_WRITES, "the grid follows the 8-dword header");
 
     // neighbourhood cell k = 9 (dz + 1) + 3 (dy + 1) + (dx + 1)
     MG_HD static float observePart(const State& s, uint32_t k) {

@@ -77,6 +77,8 @@ struct RayGrid : RayGridBase {
 };
 struct RayGridSplit : RayGridBase {
     static constexpr uint32_t OBS_SPLIT = N_RAYS;
+    // a step writes x, z, yaw and steps; the heights change on reset only
+    static constexpr uint32_t STEP_WRITES = 4;
     static constexpr const char* KERNEL = "rollout_test_raygrid_split";
 };
 
