@@ -59,11 +59,11 @@ __global__ void __launch_bounds__(256) rollout_kernel(const mg_rollout_args a) {
 }
 
 // The rollout of an env with a split observation (EnvTraits::OBS_SPLIT = K >
-// 0) whose State can be staged in LDS: a 256-thread workgroup owns E envs,
+// 0) whose State can be staged in LDS: a workgroup of NT threads owns E envs,
 // their states in LDS for the whole launch (env e at dword e * STRIDE, an odd
 // stride). Per step its first E lanes pick the action, reset if done, run
 // Env::stepState and Env::observeRest and write their slots; after a barrier
-// all 256 threads compute the E x K observation parts from the LDS states.
+// the NT threads compute the E x K observation parts from the LDS states.
 // Same draws, order and floats as rollout_kernel.
 template <typename Env>
 struct SplitRollout {
@@ -74,8 +74,8 @@ struct SplitRollout {
     static constexpr bool OK = K > 0 && !EnvTraits<Env>::STATE_IN_REGISTERS && sizeof(State) % 4 == 0 &&
                                alignof(State) <= 4;
 };
-template <typename Env, int MODE, int E>
-__global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_args a) {
+template <typename Env, int MODE, int E, int NT = 256>
+__global__ void __launch_bounds__(NT) rollout_split_kernel(const mg_rollout_args a) {
     using SR = SplitRollout<Env>;
     using State = typename Env::State;
     using Action = typename Env::Action;
@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
     const uint32_t ei = e0 + (tid < ne ? tid : 0);
     uint32_t rng = a.rng[ei];
     uint8_t done = a.done[ei];
-    states_to_lds<SD, STRIDE, E, 256>(lds, gst, ne);
+    states_to_lds<SD, STRIDE, E, NT>(lds, gst, ne);
     if (PART && tid < (uint32_t)E) reset_in[tid] = 0;
     __syncthreads();
     for (uint32_t t = 0; t < a.steps; ++t) {
@@ -127,7 +127,7 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
         }
         __syncthreads();  // every state is stepped
         const size_t row0 = ((size_t)t * n + e0) * O;
-        for (uint32_t q = tid; q < ne * K; q += 256) {
+        for (uint32_t q = tid; q < ne * K; q += NT) {
             const uint32_t e = q / K, p = q % K;
             const float v = Env::observePart(*reinterpret_cast<const State*>(lds + e * STRIDE), p);
             if (a.obs_out) a.obs_out[row0 + (size_t)e * O + p] = v;
@@ -138,41 +138,33 @@ __global__ void __launch_bounds__(256) rollout_split_kernel(const mg_rollout_arg
         a.rng[e0 + tid] = rng;
         a.done[e0 + tid] = done;
     }
-    states_from_lds<SD, STRIDE, E, 256, HW>(lds, gst, ne, reset_in);  // reset_in: after the loop's last barrier
+    states_from_lds<SD, STRIDE, E, NT, HW>(lds, gst, ne, reset_in);  // reset_in: after the loop's last barrier
 }
 
+// rollout_split_kernel with E envs per workgroup on NT = 64 ceil(E K / 64)
+// threads, so that every observation part of a step runs in one pass. Each
+// step is a chain of dependent LDS accesses and two barriers, so the kernel is
+// latency-bound and the shape decides how many envs a CU interleaves:
+//  - states over 2 KB (VoxelNav16's 4 KB grids: LDS holds 36 to 38 per CU):
+//    E = 4 on 128 threads. Random actions, 262144 envs, 32 steps: 771 us
+//    against 827 on 256 threads (8 workgroups per CU instead of 9), 870 with
+//    E = 2 on 64 threads, 1.02 ms with E = 4 on 64 (two passes of parts);
+//  - smaller states (VoxelNav's 1 KB heightmaps, whose parts are ray marches):
+//    E = 2 on one wave. 7.23 ms at 262144 envs against 7.46 with E = 8 on 128
+//    threads and 8.43 with E = 16 on 256; 515 against 626 us at 4096 envs
+//    (E = 4 on 128 threads).
 template <typename Env, int MODE, int E>
 void launch_split_e(const mg_rollout_args* a, hipStream_t st) {
-    hipLaunchKernelGGL((rollout_split_kernel<Env, MODE, E>), dim3((a->n + E - 1) / E), dim3(256), 0, st, *a);
+    constexpr int P = E * (int)SplitRollout<Env>::K;
+    constexpr int NT = P <= 64 ? 64 : P <= 128 ? 128 : 256;
+    hipLaunchKernelGGL((rollout_split_kernel<Env, MODE, E, NT>), dim3((a->n + E - 1) / E), dim3(NT), 0, st, *a);
 }
 
-// rollout_split_kernel with E envs per workgroup: at most as many as keep the
-// workgroup's staged states within 17 KB of LDS, so that eight workgroups
-// (the 32 waves a CU holds) fit a CU's 160 KB, and fewer at small n, so the
-// grid stays at 1 K to 16 K workgroups. Each step is a short chain of
-// dependent LDS accesses and two barriers, so the more workgroups a CU
-// interleaves the better: VoxelNav16 (4 KB states), random actions, 262144
-// envs: 2.56 ms per 32-step launch with 16 envs per workgroup (two per CU),
-// 1.79 with 8, 1.49 with 4 (eight per CU); 4 envs on 128 or 64 threads 1.65
-// and 2.30, one env per wave 2.0. The heightmap VoxelNav (1 KB states, 16 per
-// workgroup, in M env steps/s against one lane per env: 183 / 16.3 at 4096
-// envs with E = 4, 414 / 65 at 16384 with E = 8, 691 / 196 at 65536 and
-// 853 / 437 at 262144 with E = 16).
 template <typename Env, int MODE>
 void launch_split_rollout(const mg_rollout_args* a, hipStream_t st) {
-    constexpr uint32_t fit = 17408u / (SplitRollout<Env>::STRIDE * 4u);  // states in 17 KB
-    constexpr int EL = fit >= 16 ? 16 : fit >= 8 ? 8 : fit >= 4 ? 4 : fit >= 2 ? 2 : 1;
-    const uint32_t n = a->n;
-    const int en = n <= 4096u ? 4 : (n <= 32768u ? 8 : 16);
-    const int e = EL < en ? EL : en;  // 16, 8, 4, or EL below 4
-    if constexpr (EL >= 16)
-        if (e == 16) return launch_split_e<Env, MODE, 16>(a, st);
-    if constexpr (EL >= 8)
-        if (e == 8) return launch_split_e<Env, MODE, 8>(a, st);
-    if constexpr (EL >= 4)
-        launch_split_e<Env, MODE, 4>(a, st);
-    else
-        launch_split_e<Env, MODE, EL>(a, st);
+    constexpr uint32_t bytes = SplitRollout<Env>::STRIDE * 4u;  // LDS per staged state
+    constexpr int E = bytes > 2048u ? (bytes * 4u <= 17408u ? 4 : 1) : 2;
+    launch_split_e<Env, MODE, E>(a, st);
 }
 
 // Returns 0, a positive hipError_t on a launch failure, or MG_ERR_INVALID.

@@ -40,18 +40,19 @@ def test_random_rollout_bit_exact(mg, orc, env, n, steps, seed):
 
 
 @pytest.mark.parametrize("env,n,steps,reps,seed", [
-    ("voxelnav", 4100, 40, 7, 4),      # 8 envs per workgroup, the last workgroup partial
-    ("voxelnav", 33000, 20, 13, 5),    # 16 envs per workgroup, the last workgroup partial
-    ("voxelnav16", 4099, 40, 7, 6),    # 4 KB states: 4 per workgroup (16.5 KB of LDS), the last partial
+    ("voxelnav", 4101, 40, 7, 4),      # 1 KB states: 2 envs per one-wave workgroup, the last partial
+    ("voxelnav", 33001, 20, 13, 5),    # the same at a larger grid
+    ("voxelnav16", 4099, 40, 7, 6),    # 4 KB states: 4 per 128-thread workgroup (16.5 KB of LDS), the last partial
     ("voxelnav16", 33001, 20, 13, 7),  # 4 per workgroup at any n, the last partial
 ])
 def test_split_rollout_sizes_bit_exact(mg, orc, env, n, steps, reps, seed):
     """The split-observation rollouts (VoxelNav's ray casts, VoxelNav16's
-    neighbourhood cells, spread over each workgroup) at the env counts that
-    give VoxelNav 8 and 16 envs per workgroup, run past the 250- and 256-step
-    caps so that every env resets at least once (VoxelNav16's split reset
-    fills a workgroup's flagged grids on all its threads, several envs in one
-    step at the first step and at the cap)."""
+    neighbourhood cells, spread over each workgroup) at env counts that leave
+    the last workgroup partial, run past the 250- and 256-step caps so that
+    every env resets at least once (several envs of a workgroup in one step,
+    at the first step and at the cap); VoxelNav16 writes its grid back only
+    in a launch in which the env reset, which the later launches' observations
+    and the final states check."""
     eid, kernel = ENVS[env]
     gym = mg.Gym(kernel, n, seed)
     g = orc.GymState(eid, n, seed)
