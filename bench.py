@@ -370,8 +370,8 @@ def profile_pass(which):
     "train": one collect and two train(1) epochs of the 262144-env fp32 loop
     (2048 minibatches each, enqueued back to back as in the benchmark).
     "cfg45": configs 4 and 5 at 262144 envs: three collects and 64 minibatches
-    each of CartPoleContinuous and VoxelNav16, six VoxelNav16 random rollouts,
-    and the 1 GiB copy."""
+    each of CartPoleContinuous and VoxelNav16, eleven VoxelNav16 random rollouts
+    (their resets per launch printed), and the 1 GiB copy."""
     import metalgym_amd as mg
 
     n, T = 262144, 32
@@ -388,12 +388,20 @@ def profile_pass(which):
             sync()
             print(f"profile: 64 train minibatches of 4096 rows of {kernel}", flush=True)
             del model, gym
+        # the bench's launches (one after the gym's first, which resets every
+        # env, then ten), each env that resets in a launch counted from the done
+        # slots: such an env writes its whole 4128-byte state back
+        import numpy as np
         gym = mg.Gym("rollout_voxelnav16", n, 0)
         bufs = gym.rollout_random(T)
-        for _ in range(5):
-            gym.rollout_random(T, bufs, sync=False)
-        sync()
-        print("profile: 6 random rollouts of rollout_voxelnav16 at 262144 x 32", flush=True)
+        prev = bufs[3].download(np.uint8, (T, n))[T - 1].astype(bool)
+        resets = [n]
+        for _ in range(10):
+            gym.rollout_random(T, bufs)
+            d = bufs[3].download(np.uint8, (T, n)).astype(bool)
+            resets.append(int((prev | d[:T - 1].any(axis=0)).sum()))
+            prev = d[T - 1]
+        print(f"profile: 11 random rollouts of rollout_voxelnav16 at 262144 x 32, resets {resets}", flush=True)
         del gym, bufs
         nbytes = 1 << 30
         a, b = mg.DeviceBuffer(nbytes), mg.DeviceBuffer(nbytes)
