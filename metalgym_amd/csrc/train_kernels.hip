@@ -497,13 +497,33 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
     static_assert((kMaxObsT + 1) * kEmbed <= (MG_MAX_LAYERS + 1) * kTR * kEmbed, "embed staging fits");
     const float* lnp = pv.params + pv.off_ln_gamma[0];
     const int n_obs = M * O, n_wh = kEmbed * HD, n_win = O * kEmbed, n_ln = (NL + 1) * 2 * kEmbed;
+    // the loss inputs of this thread's row (32 threads per row)
+    const int lrow = tid >> 5, lk = tid & 31;
+    float an, oldLp, ret;
+    int act = 0;
+    Stream wst;
+    const typename RowsTypes<BF>::Seq seq{&pv, H / kChunk};
     {
-        const float o0 = tid < n_obs ? a.obs_slots[g0 * O + tid] : 0.0f;
-        const float h0 = tid < n_wh ? pv.params[pv.off_head + tid] : 0.0f;
-        const float w0 = tid < n_win ? pv.params[pv.off_in_w + tid] : 0.0f;
-        const float b0 = tid < kEmbed ? pv.params[pv.off_in_b + tid] : 0.0f;
-        const float l0 = tid < n_ln ? lnp[tid] : 0.0f;
-        const float l1 = tid + kTNT < n_ln ? lnp[tid + kTNT] : 0.0f;
+        // branch-free: a thread past an array's end loads an element in range
+        // and drops it (loads behind a range branch made the compiler wait for
+        // every outstanding load at the branch's join)
+        const float o0 = a.obs_slots[g0 * O + (tid < n_obs ? tid : n_obs - 1)];
+        const float h0 = pv.params[pv.off_head + (tid < n_wh ? tid : 0)];
+        const float w0 = pv.params[pv.off_in_w + (tid < n_win ? tid : 0)];
+        const float b0 = pv.params[pv.off_in_b + (tid < kEmbed ? tid : 0)];
+        const float l0 = lnp[tid < n_ln ? tid : 0];
+        const float l1 = lnp[tid + kTNT < n_ln ? tid + kTNT : 0];
+        {
+            const size_t gr = g0 + lrow;
+            const float mean = a.adv_stats[2 * a.step.block], inv = a.adv_stats[2 * a.step.block + 1];
+            an = (a.adv_slots[gr] - mean) * inv;
+            oldLp = a.logp_slots[gr];
+            ret = a.ret_slots[gr];
+            if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
+        }
+        // the weight stream next: its loads are in flight while the stores
+        // below wait for the small loads ahead of them
+        wst.start(4 * NL * (H / kChunk), seq);
         if (tid < n_obs) L.obs[tid] = o0;
         if (tid < n_wh) L.wh[tid] = h0;
         if (tid < n_win) winL[tid] = w0;
@@ -511,25 +531,14 @@ __global__ void __launch_bounds__(kTNT) train_rows_kernel(const RowsArgs a) {
         if (tid < n_ln) L.ln[tid] = l0;
         if (tid + kTNT < n_ln) L.ln[tid + kTNT] = l1;
     }
+#pragma unroll 4
     for (int idx = tid + kTNT; idx < n_obs; idx += kTNT) L.obs[idx] = a.obs_slots[g0 * O + idx];
+#pragma unroll 4
     for (int idx = tid + kTNT; idx < n_wh; idx += kTNT) L.wh[idx] = pv.params[pv.off_head + idx];
+#pragma unroll 4
     for (int idx = tid + kTNT; idx < n_win; idx += kTNT) winL[idx] = pv.params[pv.off_in_w + idx];
+#pragma unroll 4
     for (int idx = tid + 2 * kTNT; idx < n_ln; idx += kTNT) L.ln[idx] = lnp[idx];
-    // the loss inputs of this thread's row (32 threads per row)
-    const int lrow = tid >> 5, lk = tid & 31;
-    float an, oldLp, ret;
-    int act = 0;
-    {
-        const size_t gr = g0 + lrow;
-        const float mean = a.adv_stats[2 * a.step.block], inv = a.adv_stats[2 * a.step.block + 1];
-        an = (a.adv_slots[gr] - mean) * inv;
-        oldLp = a.logp_slots[gr];
-        ret = a.ret_slots[gr];
-        if (!pv.continuous) act = static_cast<const int*>(a.action_slots)[gr];
-    }
-    Stream wst;
-    const typename RowsTypes<BF>::Seq seq{&pv, H / kChunk};
-    wst.start(4 * NL * (H / kChunk), seq);
     __syncthreads();
 
     // ---- forward with capture ----
