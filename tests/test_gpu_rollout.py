@@ -73,22 +73,28 @@ def test_split_rollout_sizes_bit_exact(mg, orc, env, n, steps, reps, seed):
 
 @pytest.mark.parametrize("env", ["cartpole", "cartpole_continuous", "voxelnav16", "voxelnav"])
 def test_given_action_rollout_bit_exact(mg, orc, env):
+    """Given actions, launch after launch. The split-observation envs run three
+    launches of 100 steps, past their 250- and 256-step caps, so that launches
+    in which most envs do not reset (VoxelNav16 then writes back only its
+    32-byte header) are followed by ones that read the states back."""
     eid, kernel = ENVS[env]
-    n, steps = 2048, 40
+    split = env in ("voxelnav16", "voxelnav")
+    n, steps, reps = 2048, (100 if split else 40), (3 if split else 1)
     gym = mg.Gym(kernel, n, 5)
     g = orc.GymState(eid, n, 5)
     rs = np.random.default_rng(1)
-    if gym.continuous:
-        acts = (rs.standard_normal((steps, n, gym.act_dim)) * 2).astype(np.float32)
-    else:
-        acts = rs.integers(0, gym.act_dim, (steps, n)).astype(np.int32)
-    bufs = gym.rollout_given(steps, acts)
-    _, obs, rew, dn = gym.download_slots(bufs, steps)
-    _, oo, orw, od = orc.rollout(g, steps, random=False, actions_in=acts, threads=THREADS)
-    assert_bit_exact(obs, oo, "obs")
-    assert_bit_exact(rew, orw, "reward")
-    assert_bit_exact(dn, od, "done")
-    compare_gym(gym, g, env)
+    for rep in range(reps):
+        if gym.continuous:
+            acts = (rs.standard_normal((steps, n, gym.act_dim)) * 2).astype(np.float32)
+        else:
+            acts = rs.integers(0, gym.act_dim, (steps, n)).astype(np.int32)
+        bufs = gym.rollout_given(steps, acts)
+        _, obs, rew, dn = gym.download_slots(bufs, steps)
+        _, oo, orw, od = orc.rollout(g, steps, random=False, actions_in=acts, threads=THREADS)
+        assert_bit_exact(obs, oo, f"rep {rep} obs")
+        assert_bit_exact(rew, orw, f"rep {rep} reward")
+        assert_bit_exact(dn, od, f"rep {rep} done")
+        compare_gym(gym, g, f"{env} rep {rep}")
 
 
 def test_gym_run_single_steps(mg, orc):
