@@ -41,8 +41,10 @@ __device__ __forceinline__ void sample_gaussian(const float* h, const float* log
             const float u2 = (float)(rngNext(rng) >> 8) * (1.0f / 16777216.0f);
             const float r = sqrtf(-2.0f * mg::logf(u1));
             const float th = 2.0f * kPiF * u2;
-            z0 = r * mg::cosf(th);
-            z1 = r * mg::sinf(th);
+            float st, ct;
+            mg::sincosf(th, &st, &ct);  // the bits of mg::sinf and mg::cosf, one reduction
+            z0 = r * ct;
+            z1 = r * st;
         }
         const float zk = (k & 1) ? z1 : z0;
         const float ls = logStd[k];

@@ -50,8 +50,8 @@ struct CartPole {
 
     // Shared by CartPole and CartPoleContinuous: one Euler step under `force`.
     MG_HD static void integrate(State& s, float force, Obs& obs, float& reward, uint8_t& done) {
-        float cosTheta = mg::cosf(s.theta);
-        float sinTheta = mg::sinf(s.theta);
+        float sinTheta, cosTheta;
+        mg::sincosf(s.theta, &sinTheta, &cosTheta);  // the bits of mg::sinf and mg::cosf, one reduction
         float temp = (force + POLE_MASS_LENGTH * s.thetaDot * s.thetaDot * sinTheta) / TOTAL_MASS;
         float thetaAcc = (GRAVITY * sinTheta - cosTheta * temp) /
                          (LENGTH * (4.0f / 3.0f - MASS_POLE * cosTheta * cosTheta / TOTAL_MASS));

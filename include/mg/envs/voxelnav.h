@@ -114,8 +114,9 @@ struct VoxelNav {
     MG_HD static float march(const State& s, float ey, float ca, float sa, uint32_t r) {
         const float pitches[RAY_ROWS] = {-45.0f, -20.0f, 0.0f, 15.0f};
         const float p = pitches[r] * PI / 180.0f;
-        const float cp = mg::cosf(p);
-        const float dx = cp * ca, dy = mg::sinf(p), dz = cp * sa;
+        float sp, cp;
+        mg::sincosf(p, &sp, &cp);  // the bits of mg::sinf and mg::cosf, one reduction
+        const float dx = cp * ca, dy = sp, dz = cp * sa;
         constexpr uint32_t kSamples = 47;  // t = 0.5 k < MAX_DEPTH
         for (uint32_t k0 = 1; k0 <= kSamples; k0 += 4) {
             bool hit[4];
@@ -145,12 +146,15 @@ struct VoxelNav {
     MG_HD static float observePart(const State& s, uint32_t k) {
         const uint32_t c = k / RAY_ROWS, r = k % RAY_ROWS;
         const float a = rayYaw(s, c);
-        return march(s, heightAt(s, s.x, s.z) + EYE, mg::cosf(a), mg::sinf(a), r);
+        float sa, ca;
+        mg::sincosf(a, &sa, &ca);
+        return march(s, heightAt(s, s.x, s.z) + EYE, ca, sa, r);
     }
     MG_HD static void observeRest(const State& s, Obs& o) {
         const float h = heightAt(s, s.x, s.z);
         const float gx = s.gx - s.x, gz = s.gz - s.z;
-        const float ca = mg::cosf(s.yaw), sa = mg::sinf(s.yaw);
+        float sa, ca;
+        mg::sincosf(s.yaw, &sa, &ca);
         o.goalForward = (gx * ca + gz * sa) / (float)W;
         o.goalRight = (-gx * sa + gz * ca) / (float)W;
         o.goalUp = (heightAt(s, s.gx, s.gz) - h) / 8.0f;
@@ -165,7 +169,8 @@ struct VoxelNav {
         const float ey = heightAt(s, s.x, s.z) + EYE;
         for (uint32_t c = 0; c < RAY_COLS; c++) {
             const float a = rayYaw(s, c);
-            const float ca = mg::cosf(a), sa = mg::sinf(a);
+            float sa, ca;
+            mg::sincosf(a, &sa, &ca);
             for (uint32_t r = 0; r < RAY_ROWS; r++) o.ray[c * RAY_ROWS + r] = march(s, ey, ca, sa, r);
         }
         observeRest(s, o);
@@ -192,7 +197,8 @@ struct VoxelNav {
 
     // step() without its observation (the split-observation path).
     MG_HD static void stepState(State& s, Action action, float& reward, uint8_t& done) {
-        const float ca = mg::cosf(s.yaw), sa = mg::sinf(s.yaw);
+        float sa, ca;
+        mg::sincosf(s.yaw, &sa, &ca);
         bool fell = false;
         switch (action) {
             case 0: fell = tryMove(s, s.x + ca, s.z + sa); break;
