@@ -103,10 +103,21 @@ struct VoxelNav16 {
         return occupied(s, s.px + dx, s.py + dy, s.pz + dz) ? 1.0f : 0.0f;
     }
 
+    // (float)d / 15.0f for an integer d in [-15, 15] (a goal delta): the
+    // product with the float nearest 1/15 and one FMA correction give the
+    // correctly rounded quotient for each of the 31 values (checked on the
+    // host in tests/native/voxelnav16_fill.cpp), in 3 instructions instead of
+    // the 10 of an IEEE division.
+    MG_HD static float div15(int d) {
+        const float x = (float)d, r = 1.0f / 15.0f;
+        const float q = x * r;
+        return __builtin_fmaf(__builtin_fmaf(-q, 15.0f, x), r, q);
+    }
+
     MG_HD static void observeRest(const State& s, Obs& obs) {
-        obs.goal[0] = (float)(s.gx - s.px) / 15.0f;
-        obs.goal[1] = (float)(s.gy - s.py) / 15.0f;
-        obs.goal[2] = (float)(s.gz - s.pz) / 15.0f;
+        obs.goal[0] = div15(s.gx - s.px);
+        obs.goal[1] = div15(s.gy - s.py);
+        obs.goal[2] = div15(s.gz - s.pz);
     }
 
     MG_HD static void observe(const State& s, Obs& obs) {

@@ -2,8 +2,9 @@
 // reset turns each 32-bit draw into 16 cells with a multiply (bit 2 j of each
 // byte of r & (r >> 1) to byte j of a word); here the grid a reset writes is
 // compared with the cells read field by field from the same draws (cell
-// 16 w + c occupied iff 2-bit field c of draw w is 3), for many seeds.
-// Prints "0 failures" on success.
+// 16 w + c occupied iff 2-bit field c of draw w is 3), for many seeds; and
+// its goal-delta quotient div15(d) against the IEEE division (float)d / 15
+// for every d in [-15, 15]. Prints "0 failures" on success.
 #include <stdio.h>
 #include <string.h>
 
@@ -35,6 +36,16 @@ int main() {
         if (diff) {
             if (fails < 5) printf("fill mismatch: r0 %08x, %d cells\n", r0, diff);
             ++fails;
+        }
+    }
+    // volatile: the reference quotient is a run-time IEEE division, not a
+    // folded constant
+    for (int d = -15; d <= 15; ++d) {
+        volatile float x = (float)d, fifteen = 15.0f;
+        const float want = x / fifteen, got = VoxelNav16::div15(d);
+        if (memcmp(&want, &got, 4) != 0) {
+            ++fails;
+            printf("div15 mismatch: d %d, %a against %a\n", d, got, want);
         }
     }
     printf("%d failures\n", fails);
